@@ -1,0 +1,1337 @@
+// Backward engine: stable radix sort of (key, occurrence) pairs, first-
+// occurrence dedup, deterministic segment reduction and the fused sparse
+// optimizer row update.
+//
+// Kernel sequence of one call (all on the caller's stream):
+//   zero      clear histograms, tile tickets, look-back status, counters
+//   prepare   build the 32/64-bit sort key of every occurrence (invalid ->
+//             sentinel) and the digit histograms of every radix pass
+//   onesweep  one launch per 8-bit digit: stable in-tile ranking with wave64
+//             ballots, decoupled look-back across tiles, LDS-staged scatter
+//   runs      segment heads of the sorted keys -> run ids (chained scan)
+//   rank      first-occurrence order: scan of "is first occurrence" flags in
+//             occurrence order -> unique / first_indices / run -> rank
+//   update    per 64-position unit: sequential fp32 sum of each key's
+//             gradient rows in occurrence order, unit partials folded left to
+//             right by the last unit to finish, then the optimizer update
+//             (or the reduced gradient) written once per unique key
+#include "backward.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+namespace flare {
+
+int bits_for(uint64_t max_value) {
+  int b = 0;
+  while (b < 64 && (max_value >> b) != 0) ++b;
+  return b;
+}
+
+static size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool need_grad_row,
+                           bool need_aux, bool need_partials) {
+  Workspace w{};
+  w.n = n;
+  w.key_bytes = key_bytes;
+  w.tiles = static_cast<uint32_t>(ceil_div(std::max<int64_t>(n, 1), kSortTile));
+  w.units = static_cast<uint32_t>(ceil_div(std::max<int64_t>(n, 1), kReduceUnit));
+  const size_t un = static_cast<size_t>(std::max<int64_t>(n, 1));
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = align_up(off + bytes);
+    return at;
+  };
+  const size_t o_hist = take(8 * kRadix * 4);
+  const size_t o_tickets = take(16 * 4);
+  const size_t o_meta = take(4 * 4);
+  const size_t o_sort_status = take(static_cast<size_t>(8) * w.tiles * kRadix * 4);
+  const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
+  const size_t o_unit_counter = take(static_cast<size_t>(w.units) * 4);
+  w.zero_bytes = off;
+  const size_t o_k0 = take(un * key_bytes);
+  const size_t o_k1 = take(un * key_bytes);
+  const size_t o_v0 = take(un * 4);
+  const size_t o_v1 = take(un * 4);
+  const size_t o_grow = need_grad_row ? take(un * 4) : 0;
+  const size_t o_aux = need_aux ? take(un * 4) : 0;
+  const size_t o_roo = take(un * 4);
+  const size_t o_rs = take((un + 1) * 4);
+  const size_t o_rr = take(un * 4);
+  const size_t o_ufr = take(static_cast<size_t>(w.units) * 4);
+  const size_t o_part = need_partials ? take(static_cast<size_t>(w.units) * 2 * dim * 4) : 0;
+  w.total_bytes = off;
+  if (base) {
+    char *b = static_cast<char *>(base);
+    w.hist = reinterpret_cast<uint32_t *>(b + o_hist);
+    w.tickets = reinterpret_cast<uint32_t *>(b + o_tickets);
+    w.meta = reinterpret_cast<uint32_t *>(b + o_meta);
+    w.sort_status = reinterpret_cast<uint32_t *>(b + o_sort_status);
+    w.scan_status = reinterpret_cast<uint32_t *>(b + o_scan_status);
+    w.unit_counter = reinterpret_cast<uint32_t *>(b + o_unit_counter);
+    w.keys[0] = b + o_k0;
+    w.keys[1] = b + o_k1;
+    w.vals[0] = reinterpret_cast<uint32_t *>(b + o_v0);
+    w.vals[1] = reinterpret_cast<uint32_t *>(b + o_v1);
+    w.grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_grow) : nullptr;
+    w.aux = need_aux ? reinterpret_cast<float *>(b + o_aux) : nullptr;
+    w.run_of_occ = reinterpret_cast<uint32_t *>(b + o_roo);
+    w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
+    w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
+    w.unit_first_run = reinterpret_cast<uint32_t *>(b + o_ufr);
+    w.partial = need_partials ? reinterpret_cast<float *>(b + o_part) : nullptr;
+  }
+  return w;
+}
+
+namespace {
+
+// ----------------------------------------------------------------------------
+// zero
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void zero_kernel(uint4 *p, size_t n16) {
+  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n16; i += gridDim.x * 256ull)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float *p, size_t n) {
+  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += gridDim.x * 256ull) p[i] = 0.0f;
+}
+
+int launch_zero(void *p, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return FLARE_OK;
+  const size_t n16 = bytes / 16;  // every zeroed region is 256-byte aligned
+  const int grid = static_cast<int>(std::min<size_t>((n16 + 255) / 256, 4096));
+  zero_kernel<<<std::max(grid, 1), 256, 0, s>>>(static_cast<uint4 *>(p), n16);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+// ----------------------------------------------------------------------------
+// prepare: keys + histograms
+// ----------------------------------------------------------------------------
+template <typename K>
+__device__ __forceinline__ void add_histograms(uint32_t *s_hist, K key, int passes) {
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t d = static_cast<uint32_t>(key >> (p * kRadixBits)) & (kRadix - 1);
+    atomicAdd(&s_hist[p * kRadix + d], 1u);
+  }
+}
+
+__device__ __forceinline__ void flush_histograms(const uint32_t *s_hist, uint32_t *hist, int passes) {
+  for (int i = threadIdx.x; i < passes * kRadix; i += blockDim.x) {
+    const uint32_t c = s_hist[i];
+    if (c) atomicAdd(&hist[i], c);
+  }
+}
+
+// Keys from a row-index array (int64 store keys or int32 padded inverse).
+// valid: 0 <= key < key_limit and key != pad (when has_pad); else sentinel.
+template <typename SrcT>
+__global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restrict__ src, int64_t n,
+                                                          int64_t key_limit, int has_pad,
+                                                          int64_t pad, int passes,
+                                                          uint32_t *__restrict__ keys,
+                                                          uint32_t *__restrict__ run_of_occ,
+                                                          uint32_t *__restrict__ hist, int *err) {
+  __shared__ uint32_t s_hist[4 * kRadix];
+  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  __syncthreads();
+  const uint32_t sentinel = static_cast<uint32_t>(key_limit);
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
+    const int64_t v = static_cast<int64_t>(src[i]);
+    uint32_t k = sentinel;
+    if (!(has_pad && v == pad)) {
+      if (v >= 0 && v < key_limit) {
+        k = static_cast<uint32_t>(v);
+      } else {
+        record_error(err, kErrIndexOutOfRange);
+      }
+    }
+    keys[i] = k;
+    if (k == sentinel) run_of_occ[i] = kInvalidRun;
+    add_histograms(s_hist, k, passes);
+  }
+  __syncthreads();
+  flush_histograms(s_hist, hist, passes);
+}
+
+// Keys from CSR bags (table-major, bag k = t*batch + b).  The block's bag
+// boundaries are staged in LDS; each occurrence finds its bag by binary
+// search there.  Also writes the gradient row (b*T + t) and, for mean
+// pooling, the bag length of every occurrence.
+constexpr int kPrepBags = 256;
+
+template <typename IdT>
+__global__ __launch_bounds__(256) void prepare_csr_kernel(
+    const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
+    const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch, int64_t key_limit,
+    int passes, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
+    float *__restrict__ aux, uint32_t *__restrict__ run_of_occ, uint32_t *__restrict__ hist,
+    int *err) {
+  __shared__ uint32_t s_hist[4 * kRadix];
+  __shared__ int64_t s_off[kPrepBags + 1];
+  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * kPrepBags;
+  const int nb = static_cast<int>(std::min<int64_t>(kPrepBags, bags - bag0));
+  for (int i = threadIdx.x; i <= nb; i += 256) {
+    const int64_t o = offsets[bag0 + i];
+    s_off[i] = o < 0 ? 0 : (o > n ? n : o);
+    // offsets must start at 0, end at n and never decrease
+    if (o < 0 || o > n || (bag0 + i == 0 && o != 0) || (bag0 + i == bags && o != n))
+      record_error(err, kErrIndexOutOfRange);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb; i += 256)
+    if (s_off[i + 1] < s_off[i]) record_error(err, kErrIndexOutOfRange);
+  const int64_t first = s_off[0];
+  const int64_t last = s_off[nb];
+  const uint32_t sentinel = static_cast<uint32_t>(key_limit);
+  for (int64_t i = first + threadIdx.x; i < last; i += 256) {
+    int lo = 0, hi = nb;  // find bag: s_off[lo] <= i < s_off[lo+1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= i) lo = mid; else hi = mid;
+    }
+    const int64_t bag = bag0 + lo;
+    const int64_t t = bag / batch;
+    const int64_t b = bag - t * batch;
+    const int64_t id = static_cast<int64_t>(ids[i]);
+    const int64_t lo_row = row_base[t];
+    uint32_t k = sentinel;
+    if (id >= 0 && id < row_base[t + 1] - lo_row) {
+      k = static_cast<uint32_t>(lo_row + id);
+    } else {
+      record_error(err, kErrIndexOutOfRange);
+      run_of_occ[i] = kInvalidRun;
+    }
+    keys[i] = k;
+    grad_row[i] = static_cast<uint32_t>(b * num_tables + t);
+    if (aux) aux[i] = static_cast<float>(s_off[lo + 1] - s_off[lo]);
+    add_histograms(s_hist, k, passes);
+  }
+  __syncthreads();
+  flush_histograms(s_hist, hist, passes);
+}
+
+// Keys for generic dedup: (value - minimum) as unsigned, 32 or 64 bits.
+template <typename SrcT, typename K>
+__global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__restrict__ src,
+                                                             int64_t n,
+                                                             const uint64_t *__restrict__ minimum,
+                                                             int passes, K *__restrict__ keys,
+                                                             uint32_t *__restrict__ hist) {
+  // minimum != nullptr: keys are mapped to their order-preserving unsigned
+  // image and offset by the measured minimum; otherwise the caller promised
+  // 0 <= key < bound and the raw value is the key.
+  __shared__ uint32_t s_hist[8 * kRadix];
+  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  __syncthreads();
+  const uint64_t lo = minimum ? *minimum : 0;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
+    uint64_t ord;
+    if constexpr (std::is_signed<SrcT>::value) {
+      ord = static_cast<uint64_t>(static_cast<int64_t>(src[i]));
+      if (minimum) ord ^= 0x8000000000000000ull;
+    } else {
+      ord = static_cast<uint64_t>(src[i]);
+    }
+    const K k = static_cast<K>(ord - lo);
+    keys[i] = k;
+    add_histograms(s_hist, k, passes);
+  }
+  __syncthreads();
+  flush_histograms(s_hist, hist, passes);
+}
+
+// Order-preserving unsigned image of the keys: min and max (for the bit width).
+template <typename SrcT>
+__global__ __launch_bounds__(256) void minmax_kernel(const SrcT *__restrict__ src, int64_t n,
+                                                    unsigned long long *__restrict__ out) {
+  unsigned long long lo = ~0ull, hi = 0;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
+    unsigned long long ord;
+    if constexpr (std::is_signed<SrcT>::value)
+      ord = static_cast<unsigned long long>(static_cast<int64_t>(src[i])) ^ 0x8000000000000000ull;
+    else
+      ord = static_cast<unsigned long long>(src[i]);
+    lo = ord < lo ? ord : lo;
+    hi = ord > hi ? ord : hi;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long a = __shfl_xor(lo, off, 64);
+    const unsigned long long b = __shfl_xor(hi, off, 64);
+    lo = a < lo ? a : lo;
+    hi = b > hi ? b : hi;
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMin(&out[0], lo);
+    atomicMax(&out[1], hi);
+  }
+}
+
+__global__ void init_minmax_kernel(unsigned long long *out) {
+  out[0] = ~0ull;
+  out[1] = 0;
+}
+
+// ----------------------------------------------------------------------------
+// onesweep radix pass (stable)
+// ----------------------------------------------------------------------------
+template <typename K>
+__global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
+    const K *__restrict__ kin, const uint32_t *__restrict__ vin, K *__restrict__ kout,
+    uint32_t *__restrict__ vout, uint32_t n, int shift, const uint32_t *__restrict__ hist,
+    uint32_t *status, uint32_t *ticket, int *err) {
+  __shared__ uint32_t s_tile;
+  __shared__ uint32_t s_wcnt[4][kRadix];
+  __shared__ uint32_t s_tile_start[kRadix];
+  __shared__ uint32_t s_gbase[kRadix];
+  __shared__ uint32_t s_scan[8];
+  __shared__ K s_keys[kSortTile];
+  __shared__ uint32_t s_vals[kSortTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid == 0) s_tile = atomicAdd(ticket, 1u);
+  for (int i = tid; i < 4 * kRadix; i += kSortThreads) (&s_wcnt[0][0])[i] = 0;
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const uint32_t base = tile * kSortTile;
+
+  K key[kSortItems];
+  uint32_t val[kSortItems];
+  uint32_t rank[kSortItems];
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+    if (e < n) {
+      key[k] = kin[e];
+      val[k] = vin ? vin[e] : e;
+    } else {
+      key[k] = 0;
+      val[k] = 0;
+    }
+  }
+  const uint64_t lt = lanemask_lt();
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+    const bool valid = e < n;
+    const uint32_t d = valid ? (static_cast<uint32_t>(key[k] >> shift) & (kRadix - 1)) : 0;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    const uint32_t before = __popcll(peers & lt);
+    const uint32_t c = valid ? s_wcnt[wave][d] : 0;
+    rank[k] = c + before;
+    if (valid && before == 0) s_wcnt[wave][d] = c + static_cast<uint32_t>(__popcll(peers));
+  }
+  __syncthreads();
+
+  // per digit: wave-exclusive prefixes, tile totals, tile-local and global bases
+  const int d = tid;  // kRadix == kSortThreads
+  const uint32_t c0 = s_wcnt[0][d], c1 = s_wcnt[1][d], c2 = s_wcnt[2][d], c3 = s_wcnt[3][d];
+  const uint32_t total = c0 + c1 + c2 + c3;
+  s_wcnt[0][d] = 0;
+  s_wcnt[1][d] = c0;
+  s_wcnt[2][d] = c0 + c1;
+  s_wcnt[3][d] = c0 + c1 + c2;
+  const uint32_t tile_start = block_exclusive_scan_256(total, s_scan, nullptr);
+  const uint32_t digit_base = block_exclusive_scan_256(hist[d], s_scan + 4, nullptr);
+  const uint32_t prefix = lookback_exclusive(status, tile, kRadix, d, total, err);
+  s_tile_start[d] = tile_start;
+  s_gbase[d] = digit_base + prefix;
+  __syncthreads();
+
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+    if (e < n) {
+      const uint32_t dk = static_cast<uint32_t>(key[k] >> shift) & (kRadix - 1);
+      const uint32_t pos = s_tile_start[dk] + s_wcnt[wave][dk] + rank[k];
+      s_keys[pos] = key[k];
+      s_vals[pos] = val[k];
+    }
+  }
+  __syncthreads();
+  const uint32_t count = (n - base) < static_cast<uint32_t>(kSortTile) ? (n - base) : kSortTile;
+  for (uint32_t p = tid; p < count; p += kSortThreads) {
+    const K kk = s_keys[p];
+    const uint32_t dk = static_cast<uint32_t>(kk >> shift) & (kRadix - 1);
+    const uint32_t out = s_gbase[dk] + (p - s_tile_start[dk]);
+    if (out < n) {  // always true unless a spin guard tripped
+      kout[out] = kk;
+      vout[out] = s_vals[p];
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Block-wide inclusive count of per-element flags for a striped tile
+// (element of item k, thread t = base + k*256 + t).  Returns per item the
+// inclusive count within the tile; *tile_total gets the tile's count.
+// ----------------------------------------------------------------------------
+struct FlagScan {
+  uint32_t incl[kSortItems];
+};
+
+__device__ __forceinline__ void tile_flag_scan(const bool (&flag)[kSortItems], uint32_t *s_cnt,
+                                               FlagScan &out, uint32_t *tile_total) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint64_t le = lanemask_lt() | (1ull << lane);
+  uint32_t within[kSortItems];
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint64_t b = __ballot(flag[k]);
+    within[k] = __popcll(b & le);
+    if (lane == 0) s_cnt[k * 4 + wave] = __popcll(b);
+  }
+  __syncthreads();
+  if (tid < 64) {  // 64 counts in (item, wave) order -> exclusive scan
+    const uint32_t v = s_cnt[tid];
+    uint32_t incl = v;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += y;
+    }
+    s_cnt[64 + tid] = incl - v;
+    if (tid == 63) s_cnt[128] = incl;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) out.incl[k] = s_cnt[64 + k * 4 + wave] + within[k];
+  *tile_total = s_cnt[128];
+}
+
+// ----------------------------------------------------------------------------
+// runs: segment heads of the sorted keys
+// ----------------------------------------------------------------------------
+template <typename K>
+__global__ __launch_bounds__(kSortThreads) void runs_kernel(
+    const K *__restrict__ sk, const uint32_t *__restrict__ sv, uint32_t n, K sentinel,
+    int use_sentinel, uint32_t *__restrict__ run_start, uint32_t *__restrict__ unit_first_run,
+    uint32_t *__restrict__ run_of_occ, uint32_t *__restrict__ meta, uint32_t *status,
+    uint32_t *ticket, int *err) {
+  __shared__ uint32_t s_tile;
+  __shared__ uint32_t s_cnt[160];
+  __shared__ uint32_t s_prefix;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_tile = atomicAdd(ticket, 1u);
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const uint32_t base = tile * kSortTile;
+  bool valid[kSortItems], head[kSortItems];
+  K key[kSortItems];
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t j = base + k * kSortThreads + tid;
+    valid[k] = false;
+    head[k] = false;
+    if (j < n) {
+      key[k] = sk[j];
+      valid[k] = !(use_sentinel && key[k] == sentinel);
+      head[k] = valid[k] && (j == 0 || sk[j - 1] != key[k]);
+    }
+  }
+  FlagScan fs;
+  uint32_t total;
+  tile_flag_scan(head, s_cnt, fs, &total);
+  if (tid == 0) s_prefix = lookback_exclusive(status, tile, 1, 0, total, err);
+  __syncthreads();
+  const uint32_t prefix = s_prefix;
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t j = base + k * kSortThreads + tid;
+    if (!valid[k]) {
+      if (j == 0 && j < n) {  // nothing valid at all
+        meta[0] = 0;
+        meta[1] = 0;
+        run_start[0] = 0;
+      }
+      continue;
+    }
+    const uint32_t r = prefix + fs.incl[k] - 1;
+    if (r >= n) continue;  // only after a tripped spin guard
+    if (head[k]) run_start[r] = j;
+    if ((j % kReduceUnit) == 0) unit_first_run[j / kReduceUnit] = r;
+    const uint32_t o = sv[j];
+    if (o < n) run_of_occ[o] = r | (head[k] ? kHeadBit : 0u);
+    const bool last = (j + 1 == n) || (use_sentinel && sk[j + 1] == sentinel);
+    if (last) {
+      meta[0] = j + 1;
+      meta[1] = r + 1;
+      run_start[r + 1] = j + 1;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// rank: first-occurrence order
+// ----------------------------------------------------------------------------
+enum UniqueSource : int { kUniqueNone = 0, kUniqueFromValues = 1, kUniqueFromSorted = 2 };
+
+__global__ __launch_bounds__(kSortThreads) void rank_kernel(
+    const uint32_t *__restrict__ run_of_occ, uint32_t n, uint32_t *status, uint32_t *ticket,
+    uint32_t tiles, int *err, uint32_t *__restrict__ run_rank, int64_t *__restrict__ first_indices,
+    void *__restrict__ unique_out, int unique_source, const void *__restrict__ values,
+    int value_bytes, const uint32_t *__restrict__ sorted_keys,
+    const uint32_t *__restrict__ run_start, int64_t *__restrict__ unique_count) {
+  __shared__ uint32_t s_tile;
+  __shared__ uint32_t s_cnt[160];
+  __shared__ uint32_t s_prefix;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_tile = atomicAdd(ticket, 1u);
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const uint32_t base = tile * kSortTile;
+  bool first[kSortItems];
+  uint32_t ro[kSortItems];
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t i = base + k * kSortThreads + tid;
+    ro[k] = (i < n) ? run_of_occ[i] : kInvalidRun;
+    first[k] = (ro[k] & kHeadBit) != 0;
+  }
+  FlagScan fs;
+  uint32_t total;
+  tile_flag_scan(first, s_cnt, fs, &total);
+  if (tid == 0) {
+    const uint32_t p = lookback_exclusive(status, tile, 1, 0, total, err);
+    s_prefix = p;
+    if (tile == tiles - 1 && unique_count) *unique_count = static_cast<int64_t>(p + total);
+  }
+  __syncthreads();
+  const uint32_t prefix = s_prefix;
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    if (!first[k]) continue;
+    const uint32_t i = base + k * kSortThreads + tid;
+    const uint32_t rank = prefix + fs.incl[k] - 1;
+    const uint32_t r = ro[k] & ~kHeadBit;
+    if (rank >= n || r >= n) continue;  // only after a tripped spin guard
+    run_rank[r] = rank;
+    if (first_indices) first_indices[rank] = i;
+    if (unique_source == kUniqueFromValues) {
+      if (value_bytes == 8)
+        static_cast<uint64_t *>(unique_out)[rank] = static_cast<const uint64_t *>(values)[i];
+      else
+        static_cast<uint32_t *>(unique_out)[rank] = static_cast<const uint32_t *>(values)[i];
+    } else if (unique_source == kUniqueFromSorted) {
+      const uint32_t at = run_start[r];
+      if (at < n) static_cast<int64_t *>(unique_out)[rank] = static_cast<int64_t>(sorted_keys[at]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void inverse_kernel(const uint32_t *__restrict__ run_of_occ,
+                                                     const uint32_t *__restrict__ run_rank,
+                                                     int64_t n, int32_t *__restrict__ inverse) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
+    const uint32_t ro = run_of_occ[i];
+    inverse[i] = (ro == kInvalidRun) ? -1 : static_cast<int32_t>(run_rank[ro & ~kHeadBit]);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// update: deterministic segment reduction + optimizer
+// ----------------------------------------------------------------------------
+enum ApplyMode : int { kModeRows = 0, kModeUnique = 1, kModeSgd = 2, kModeAdam = 3, kModeAdagrad = 4 };
+enum GradRowMode : int { kGradRowOcc = 0, kGradRowDiv = 1, kGradRowArray = 2 };
+enum ScaleMode : int { kScaleNone = 0, kScaleMul = 1, kScaleDiv = 2 };
+
+struct UpdateArgs {
+  const uint32_t *sk;
+  const uint32_t *sv;
+  const uint32_t *run_start;
+  const uint32_t *unit_first_run;
+  const uint32_t *meta;
+  const uint32_t *run_rank;
+  int32_t *inverse_out;
+  const float *grad;
+  int grad_mode;
+  uint32_t grad_div;
+  const uint32_t *grad_row;
+  int scale_mode;
+  const float *scale;  // weights (kScaleMul) or divisors (kScaleDiv), per occurrence
+  int use_norm;
+  float norm;
+  int dim;
+  float *partial;
+  uint32_t *unit_counter;
+  float *out;
+  void *table;
+  float *s0;
+  float *s1;
+  int32_t *step;
+  float lr, eps, b1, b2, omb1, omb2;
+  double b1d, b2d;
+  uint32_t units;
+  uint32_t n;
+  int *err;
+};
+
+template <int G>
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+  for (int m = G / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, G);
+  return v;
+}
+
+template <typename Tag, int VEC, int G, int NC, int MODE>
+__device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, uint32_t key,
+                                             float (&g)[NC][VEC], int lane) {
+  const int D = a.dim;
+  if (a.use_norm) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) g[c][v] = g[c][v] / a.norm;
+  }
+  if constexpr (MODE == kModeRows || MODE == kModeUnique) {
+    const int64_t row = (MODE == kModeRows) ? static_cast<int64_t>(key)
+                                            : static_cast<int64_t>(a.run_rank[r]);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (col < D) store_f32<VEC>(a.out + row * D + col, g[c]);
+    }
+  } else {
+    using E = typename Tag::elem;
+    E *table = static_cast<E *>(a.table);
+    const int64_t row = key;
+    if constexpr (MODE == kModeAdagrad) {
+      double ss = 0.0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col < D)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) ss += static_cast<double>(g[c][v]) * static_cast<double>(g[c][v]);
+      }
+      ss = group_sum<G>(ss);
+      const float accn = static_cast<float>(static_cast<double>(a.s0[row]) + ss / static_cast<double>(D));
+      const float den = sqrtf(accn) + a.eps;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col >= D) continue;
+        float w[VEC];
+        load_as_f32<Tag, VEC>(table + row * D + col, w);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) w[v] = w[v] - (a.lr * g[c][v]) / den;
+        store_from_f32<Tag, VEC>(table + row * D + col, w);
+      }
+      if (lane == 0) a.s0[row] = accn;
+    } else if constexpr (MODE == kModeSgd) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col >= D) continue;
+        float w[VEC];
+        load_as_f32<Tag, VEC>(table + row * D + col, w);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) w[v] = w[v] - a.lr * g[c][v];
+        store_from_f32<Tag, VEC>(table + row * D + col, w);
+      }
+    } else {  // Adam
+      const int32_t st = a.step[row] + 1;
+      const float bc1 = static_cast<float>(1.0 - pow(a.b1d, static_cast<double>(st)));
+      const float bc2 = static_cast<float>(1.0 - pow(a.b2d, static_cast<double>(st)));
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col >= D) continue;
+        float w[VEC], m[VEC], v2[VEC];
+        load_as_f32<Tag, VEC>(table + row * D + col, w);
+        load_f32<VEC>(a.s0 + row * D + col, m);
+        load_f32<VEC>(a.s1 + row * D + col, v2);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          const float gv = g[c][v];
+          m[v] = a.b1 * m[v] + a.omb1 * gv;
+          v2[v] = a.b2 * v2[v] + a.omb2 * (gv * gv);
+          const float mh = m[v] / bc1;
+          const float vh = v2[v] / bc2;
+          w[v] = w[v] - (a.lr * mh) / (sqrtf(vh) + a.eps);
+        }
+        store_f32<VEC>(a.s0 + row * D + col, m);
+        store_f32<VEC>(a.s1 + row * D + col, v2);
+        store_from_f32<Tag, VEC>(table + row * D + col, w);
+      }
+      if (lane == 0) a.step[row] = st;
+    }
+  }
+}
+
+template <typename Tag, int VEC, int G, int NC, int MODE>
+__global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
+  constexpr int kGroups = 256 / G;
+  constexpr int kPPL = kReduceUnit / G;  // sorted positions per lane in the prefetch
+  __shared__ uint32_t s_grow[kGroups][kReduceUnit];
+  __shared__ float s_scale[kGroups][kReduceUnit];
+
+  const int lane = threadIdx.x % G;
+  const int group = threadIdx.x / G;
+  const int group_lane0 = (threadIdx.x & 63) - lane;  // first lane of this group in the wave
+  const uint32_t u = blockIdx.x * kGroups + group;
+  const uint32_t nvalid = a.meta[0];
+  const uint32_t j0 = u * kReduceUnit;
+  const bool active = (u < a.units) && (j0 < nvalid);
+  const uint32_t j1 = active ? min(j0 + kReduceUnit, nvalid) : j0;
+  const int cnt = static_cast<int>(j1 - j0);
+  const int D = a.dim;
+
+  // Prefetch occurrence, gradient row and scale of every position of the unit.
+  uint32_t occ[kPPL];
+  uint64_t heads = 0;
+#pragma unroll
+  for (int q = 0; q < kPPL; ++q) {
+    const int p = q * G + lane;
+    bool head = false;
+    occ[q] = 0;
+    if (p < cnt) {
+      const uint32_t j = j0 + p;
+      uint32_t o = a.sv[j];
+      if (o >= a.n) {  // only if the sort was corrupted (tripped spin guard)
+        record_error(a.err, kErrSpinGuard);
+        o = 0;
+      }
+      occ[q] = o;
+      head = (j == 0) || (a.sk[j] != a.sk[j - 1]);
+      uint32_t gr = o;
+      if (a.grad_mode == kGradRowDiv) gr = o / a.grad_div;
+      else if (a.grad_mode == kGradRowArray) gr = a.grad_row[o];
+      s_grow[group][p] = gr;
+      s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f : a.scale[o];
+    }
+    const uint64_t bal = __ballot(head);
+    const uint64_t mine = (G == 64) ? bal : ((bal >> group_lane0) & ((1ull << G) - 1));
+    heads |= mine << (q * G);
+  }
+  __syncthreads();
+  if (!active) return;
+
+  uint32_t r = a.unit_first_run[u];
+  int p = 0;
+  while (p < cnt) {
+    // end of this piece: next head after p, or the end of the unit
+    const uint64_t later = (p + 1 < 64) ? (heads & (~0ull << (p + 1))) : 0ull;
+    const int e = later ? min(static_cast<int>(__builtin_ctzll(later)), cnt) : cnt;
+    float acc[NC][VEC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
+    for (int pp = p; pp < e; pp += 4) {
+      float x[4][NC][VEC];
+      float sc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bool ok = pp + t < e;
+        const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pp + t]) : 0;
+        sc[t] = ok ? s_scale[group][pp + t] : 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (ok && col < D) {
+            load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
+          } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (pp + t >= e) break;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            float y = x[t][c][v];
+            if (a.scale_mode == kScaleMul) y = y * sc[t];
+            else if (a.scale_mode == kScaleDiv) y = y / sc[t];
+            acc[c][v] += y;
+          }
+      }
+    }
+
+    // finish the piece of run r
+    const uint32_t seg_start = a.run_start[r];
+    const uint32_t seg_end = a.run_start[r + 1];
+    bool do_apply = true;
+    if (!(seg_start >= j0 && seg_end <= j1)) {
+      // the key spans several units: publish this unit's partial
+      const int slot = (seg_start < j0) ? 0 : 1;
+      float *mine = a.partial + (static_cast<size_t>(u) * 2 + slot) * D;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col < D) store_f32<VEC>(mine + col, acc[c]);
+      }
+      __threadfence();
+      const uint32_t h = seg_start / kReduceUnit;
+      const uint32_t t_unit = (seg_end - 1) / kReduceUnit;
+      uint32_t old = 0;
+      if (lane == 0) old = atomicAdd(&a.unit_counter[h], 1u);
+      old = __shfl(old, 0, G);
+      do_apply = (old == t_unit - h);
+      if (do_apply) {
+        __threadfence();
+        const float *ph = a.partial + (static_cast<size_t>(h) * 2 + 1) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (col < D) load_f32<VEC>(ph + col, acc[c]);
+        }
+        for (uint32_t x = h + 1; x <= t_unit; ++x) {
+          const float *px = a.partial + (static_cast<size_t>(x) * 2 + 0) * D;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (col < D) {
+              float y[VEC];
+              load_f32<VEC>(px + col, y);
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[c][v] += y[v];
+            }
+          }
+        }
+      }
+    }
+    if (do_apply) apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
+    ++r;
+    p = e;
+  }
+
+  if (a.inverse_out) {
+    const uint32_t r0 = a.unit_first_run[u];
+#pragma unroll
+    for (int q = 0; q < kPPL; ++q) {
+      const int pos = q * G + lane;
+      if (pos < cnt) {
+        const uint64_t upto = (pos == 63) ? ~0ull : ((2ull << pos) - 1);
+        const uint32_t rr = r0 + __popcll(heads & upto & ~1ull);
+        a.inverse_out[occ[q]] = static_cast<int32_t>(a.run_rank[rr]);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// host orchestration
+// ----------------------------------------------------------------------------
+struct Shape {
+  int vec;
+  int g;
+  int nc;
+};
+
+int choose_shape(int dim, bool vec4_ok, Shape *out) {
+  const int vec = (vec4_ok && dim % 4 == 0) ? 4 : 1;
+  const int cols = dim / vec;
+  if (cols <= 64) {
+    int g = 8;
+    while (g < cols) g <<= 1;
+    *out = {vec, g, 1};
+    return FLARE_OK;
+  }
+  int nc = 2;
+  while (nc * 64 < cols) nc <<= 1;
+  if (nc > 8) return fail(FLARE_ERR_LIMIT, "embedding dim %d exceeds the supported maximum (%d)", dim, vec * 512);
+  *out = {vec, 64, nc};
+  return FLARE_OK;
+}
+
+template <typename Tag, int VEC, int MODE>
+int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
+  auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
+  if (sh.nc == 1) {
+    switch (sh.g) {
+      case 8: update_kernel<Tag, VEC, 8, 1, MODE><<<grid(8), 256, 0, s>>>(a); break;
+      case 16: update_kernel<Tag, VEC, 16, 1, MODE><<<grid(16), 256, 0, s>>>(a); break;
+      case 32: update_kernel<Tag, VEC, 32, 1, MODE><<<grid(32), 256, 0, s>>>(a); break;
+      default: update_kernel<Tag, VEC, 64, 1, MODE><<<grid(64), 256, 0, s>>>(a); break;
+    }
+  } else {
+    switch (sh.nc) {
+      case 2: update_kernel<Tag, VEC, 64, 2, MODE><<<grid(64), 256, 0, s>>>(a); break;
+      case 4: update_kernel<Tag, VEC, 64, 4, MODE><<<grid(64), 256, 0, s>>>(a); break;
+      default: update_kernel<Tag, VEC, 64, 8, MODE><<<grid(64), 256, 0, s>>>(a); break;
+    }
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+template <typename Tag, int MODE>
+int launch_update_tag(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
+  if (sh.vec == 4) return launch_update_vec<Tag, 4, MODE>(a, sh, s);
+  return launch_update_vec<Tag, 1, MODE>(a, sh, s);
+}
+
+int launch_update(int mode, int dtype, const UpdateArgs &a, const Shape &sh, hipStream_t s) {
+  if (mode == kModeRows) return launch_update_tag<TagF32, kModeRows>(a, sh, s);
+  if (mode == kModeUnique) return launch_update_tag<TagF32, kModeUnique>(a, sh, s);
+  switch (dtype) {
+    case FLARE_FLOAT32:
+      if (mode == kModeSgd) return launch_update_tag<TagF32, kModeSgd>(a, sh, s);
+      if (mode == kModeAdam) return launch_update_tag<TagF32, kModeAdam>(a, sh, s);
+      return launch_update_tag<TagF32, kModeAdagrad>(a, sh, s);
+    case FLARE_FLOAT16:
+      if (mode == kModeSgd) return launch_update_tag<TagF16, kModeSgd>(a, sh, s);
+      if (mode == kModeAdam) return launch_update_tag<TagF16, kModeAdam>(a, sh, s);
+      return launch_update_tag<TagF16, kModeAdagrad>(a, sh, s);
+    case FLARE_BFLOAT16:
+      if (mode == kModeSgd) return launch_update_tag<TagBF16, kModeSgd>(a, sh, s);
+      if (mode == kModeAdam) return launch_update_tag<TagBF16, kModeAdam>(a, sh, s);
+      return launch_update_tag<TagBF16, kModeAdagrad>(a, sh, s);
+    default:
+      return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", dtype);
+  }
+}
+
+// Sort keys[0]/implicit iota by the low `bits` bits; returns the buffer index
+// holding the result (0 or 1).
+template <typename K>
+int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result) {
+  const int passes = std::max(1, (bits + kRadixBits - 1) / kRadixBits);
+  const uint32_t n = static_cast<uint32_t>(w.n);
+  int cur = 0;
+  for (int p = 0; p < passes; ++p) {
+    onesweep_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
+        static_cast<const K *>(w.keys[cur]), p == 0 ? nullptr : w.vals[cur],
+        static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p * kRadixBits,
+        w.hist + p * kRadix, w.sort_status + static_cast<size_t>(p) * w.tiles * kRadix,
+        w.tickets + p, err);
+    FLARE_TRY_HIP(hipGetLastError());
+    cur ^= 1;
+  }
+  *result = cur;
+  return FLARE_OK;
+}
+
+int sort_passes(int bits) { return std::max(1, (bits + kRadixBits - 1) / kRadixBits); }
+
+// After prepare: sort, runs, rank.  Sorted u32 keys/vals are left in
+// w.keys[*sorted] / w.vals[*sorted].
+int dedup_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipStream_t s,
+               int *sorted, int64_t *first_indices, void *unique_out, int unique_source,
+               const void *values, int value_bytes, int64_t *unique_count) {
+  FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, sorted));
+  const uint32_t n = static_cast<uint32_t>(w.n);
+  const uint32_t *sk = static_cast<const uint32_t *>(w.keys[*sorted]);
+  runs_kernel<uint32_t><<<w.tiles, kSortThreads, 0, s>>>(
+      sk, w.vals[*sorted], n, sentinel, 1, w.run_start, w.unit_first_run, w.run_of_occ, w.meta,
+      w.scan_status, w.tickets + 8, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
+      w.run_of_occ, n, w.scan_status + w.tiles, w.tickets + 9, w.tiles, err, w.run_rank,
+      first_indices, unique_out, unique_source, values, value_bytes, sk, w.run_start,
+      unique_count);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+int optimizer_mode(const flare_optimizer *opt, int *mode) {
+  if (!opt) return fail(FLARE_ERR_ARGUMENT, "optimizer configuration is required");
+  if (opt->weight_decay != 0.0)
+    return fail(FLARE_ERR_ARGUMENT, "sparse optimizer weight_decay must be 0, got %g", opt->weight_decay);
+  switch (opt->kind) {
+    case FLARE_OPT_NONE: *mode = kModeUnique; return FLARE_OK;
+    case FLARE_OPT_SGD: *mode = kModeSgd; return FLARE_OK;
+    case FLARE_OPT_ADAM: *mode = kModeAdam; return FLARE_OK;
+    case FLARE_OPT_ROWWISE_ADAGRAD: *mode = kModeAdagrad; return FLARE_OK;
+    default: return fail(FLARE_ERR_ARGUMENT, "unsupported sparse optimizer kind %d", opt->kind);
+  }
+}
+
+void fill_optimizer(UpdateArgs &a, const flare_optimizer *opt) {
+  a.lr = static_cast<float>(opt->learning_rate);
+  a.eps = static_cast<float>(opt->eps);
+  a.b1 = static_cast<float>(opt->beta1);
+  a.b2 = static_cast<float>(opt->beta2);
+  a.omb1 = static_cast<float>(1.0 - opt->beta1);
+  a.omb2 = static_cast<float>(1.0 - opt->beta2);
+  a.b1d = opt->beta1;
+  a.b2d = opt->beta2;
+}
+
+int check_state(int mode, float *s0, float *s1, int32_t *step) {
+  if (mode == kModeAdagrad && !s0) return fail(FLARE_ERR_ARGUMENT, "row-wise Adagrad requires the accumulator state");
+  if (mode == kModeAdam && (!s0 || !s1 || !step))
+    return fail(FLARE_ERR_ARGUMENT, "Adam requires m, v and step state");
+  return FLARE_OK;
+}
+
+int check_workspace(const Workspace &need, size_t have) {
+  if (have < need.total_bytes)
+    return fail(FLARE_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", have, need.total_bytes);
+  return FLARE_OK;
+}
+
+bool vec4_ok(const void *p) { return aligned(p, 16); }
+
+// Shared tail of the keyed-row entry points (scatter, scatter_pooled, sparse_update).
+int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipStream_t s, int mode,
+                int dtype, int dim, const float *grad, int grad_mode, uint32_t grad_div,
+                float *out, void *table, float *s0, float *s1, int32_t *step,
+                const flare_optimizer *opt, int32_t norm_steps) {
+  int sorted = 0;
+  FLARE_TRY(dedup_rows(w, bits, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
+                       0, nullptr));
+  UpdateArgs a{};
+  a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
+  a.sv = w.vals[sorted];
+  a.run_start = w.run_start;
+  a.unit_first_run = w.unit_first_run;
+  a.meta = w.meta;
+  a.run_rank = w.run_rank;
+  a.grad = grad;
+  a.grad_mode = grad_mode;
+  a.grad_div = grad_div;
+  a.scale_mode = kScaleNone;
+  a.use_norm = norm_steps != 1;
+  a.norm = static_cast<float>(norm_steps);
+  a.dim = dim;
+  a.partial = w.partial;
+  a.unit_counter = w.unit_counter;
+  a.out = out;
+  a.table = table;
+  a.s0 = s0;
+  a.s1 = s1;
+  a.step = step;
+  if (opt) fill_optimizer(a, opt);
+  a.units = w.units;
+  a.n = static_cast<uint32_t>(w.n);
+  a.err = err;
+  const bool v4 = vec4_ok(grad) && (out ? vec4_ok(out) : true) && (table ? aligned(table, 8) : true) &&
+                  (mode == kModeAdam ? (vec4_ok(s0) && vec4_ok(s1)) : true) && vec4_ok(w.partial);
+  Shape sh;
+  FLARE_TRY(choose_shape(dim, v4, &sh));
+  return launch_update(mode, dtype, a, sh, s);
+}
+
+}  // namespace
+}  // namespace flare
+
+using namespace flare;
+
+// ----------------------------------------------------------------------------
+// scatter / scatter_pooled
+// ----------------------------------------------------------------------------
+extern "C" size_t flare_scatter_workspace_bytes(int64_t slots, int64_t emb_rows, int32_t dim) {
+  (void)emb_rows;
+  return layout_workspace(nullptr, slots, 4, std::max(dim, 1), false, false, true).total_bytes;
+}
+
+static int scatter_common(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
+                          int32_t pad_index, const float *grad, uint32_t grad_div, float *out,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  if (dim <= 0 || emb_rows < 0 || slots < 0) return fail(FLARE_ERR_SHAPE, "invalid scatter sizes");
+  if (slots > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many inverse slots (%lld)", static_cast<long long>(slots));
+  if (emb_rows >= 0xffffffffll) return fail(FLARE_ERR_LIMIT, "too many embedding rows");
+  hipStream_t s = as_stream(stream);
+  if (emb_rows > 0) {
+    const size_t n = static_cast<size_t>(emb_rows) * dim;
+    const int grid = static_cast<int>(std::min<size_t>((n + 255) / 256, 8192));
+    zero_f32_kernel<<<std::max(grid, 1), 256, 0, s>>>(out, n);
+    FLARE_TRY_HIP(hipGetLastError());
+  }
+  if (slots == 0 || emb_rows == 0) return FLARE_OK;
+  Workspace w = layout_workspace(workspace, slots, 4, dim, false, false, true);
+  FLARE_TRY(check_workspace(w, workspace_bytes));
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  const uint32_t sentinel = static_cast<uint32_t>(emb_rows);
+  const int bits = bits_for(sentinel);
+  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(slots, 256), 2048));
+  prepare_rows_kernel<int32_t><<<grid, 256, 0, s>>>(inverse, slots, emb_rows, 1, pad_index,
+                                                   sort_passes(bits),
+                                                   static_cast<uint32_t *>(w.keys[0]),
+                                                   w.run_of_occ, w.hist, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  return reduce_rows(w, bits, sentinel, err, s, kModeRows, FLARE_FLOAT32, dim, grad,
+                     grad_div == 1 ? kGradRowOcc : kGradRowDiv, grad_div, out, nullptr, nullptr,
+                     nullptr, nullptr, nullptr, 1);
+}
+
+extern "C" int flare_scatter(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
+                             int32_t pad_index, const float *grad, float *out, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad, 1, out, workspace,
+                        workspace_bytes, stream);
+}
+
+extern "C" int flare_scatter_pooled(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                                    int64_t slots, int32_t pad_index, const float *grad,
+                                    int64_t batch, int32_t features, int32_t max_elements,
+                                    float *out, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  if (features <= 0 || max_elements <= 0)
+    return fail(FLARE_ERR_WIDTH, "Sparse embedding pooled operations require positive target widths, got (%d, %d).", features, max_elements);
+  if (slots != batch * features * static_cast<int64_t>(max_elements))
+    return fail(FLARE_ERR_SHAPE, "pooled scatter inverse slots must match gradient rows times max_elements");
+  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad,
+                        static_cast<uint32_t>(max_elements), out, workspace, workspace_bytes,
+                        stream);
+}
+
+// ----------------------------------------------------------------------------
+// unique_first_occurrence
+// ----------------------------------------------------------------------------
+extern "C" size_t flare_unique_workspace_bytes(int64_t n, int32_t key_dtype) {
+  (void)key_dtype;
+  return layout_workspace(nullptr, n, 8, 1, false, false, false).total_bytes + 256;
+}
+
+namespace flare {
+namespace {
+template <typename SrcT>
+int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_out,
+                 int32_t *inverse_out, int64_t *first_indices_out, int64_t *unique_count,
+                 void *workspace, size_t workspace_bytes, hipStream_t s) {
+  Workspace w8 = layout_workspace(workspace, n, 8, 1, false, false, false);
+  FLARE_TRY(check_workspace(w8, workspace_bytes > 256 ? workspace_bytes - 256 : 0));
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  unsigned long long *mm = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace) + w8.total_bytes);
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n, 256), 2048));
+  uint64_t range;
+  const uint64_t *minimum = nullptr;
+  if (key_bound > 0) {
+    range = static_cast<uint64_t>(key_bound - 1);
+  } else {
+    init_minmax_kernel<<<1, 1, 0, s>>>(mm);
+    minmax_kernel<SrcT><<<grid, 256, 0, s>>>(values, n, mm);
+    FLARE_TRY_HIP(hipGetLastError());
+    unsigned long long host[2];
+    FLARE_TRY_HIP(hipMemcpyAsync(host, mm, sizeof(host), hipMemcpyDeviceToHost, s));
+    FLARE_TRY_HIP(hipStreamSynchronize(s));
+    range = host[1] - host[0];
+    minimum = reinterpret_cast<const uint64_t *>(mm);
+  }
+  const int bits = bits_for(range);
+  const int passes = sort_passes(bits);
+  const int value_bytes = sizeof(SrcT);
+  if (bits <= 32) {
+    // same base pointer, 4-byte keys
+    Workspace w = layout_workspace(workspace, n, 4, 1, false, false, false);
+    FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+    prepare_generic_kernel<SrcT, uint32_t><<<grid, 256, 0, s>>>(values, n, minimum, passes,
+                                                                static_cast<uint32_t *>(w.keys[0]), w.hist);
+    FLARE_TRY_HIP(hipGetLastError());
+    int sorted = 0;
+    FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, &sorted));
+    runs_kernel<uint32_t><<<w.tiles, kSortThreads, 0, s>>>(
+        static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n), 0u, 0,
+        w.run_start, w.unit_first_run, w.run_of_occ, w.meta, w.scan_status, w.tickets + 8, err);
+    FLARE_TRY_HIP(hipGetLastError());
+    rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
+        w.run_of_occ, static_cast<uint32_t>(n), w.scan_status + w.tiles, w.tickets + 9, w.tiles, err,
+        w.run_rank, first_indices_out, unique_out, kUniqueFromValues, values, value_bytes, nullptr,
+        w.run_start, unique_count);
+    FLARE_TRY_HIP(hipGetLastError());
+    inverse_kernel<<<grid, 256, 0, s>>>(w.run_of_occ, w.run_rank, n, inverse_out);
+    FLARE_TRY_HIP(hipGetLastError());
+    return FLARE_OK;
+  }
+  Workspace w = w8;
+  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  prepare_generic_kernel<SrcT, uint64_t><<<grid, 256, 0, s>>>(values, n, minimum, passes,
+                                                              static_cast<uint64_t *>(w.keys[0]), w.hist);
+  FLARE_TRY_HIP(hipGetLastError());
+  int sorted = 0;
+  FLARE_TRY(run_sort<uint64_t>(w, bits, err, s, &sorted));
+  runs_kernel<uint64_t><<<w.tiles, kSortThreads, 0, s>>>(
+      static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n), 0ull, 0,
+      w.run_start, w.unit_first_run, w.run_of_occ, w.meta, w.scan_status, w.tickets + 8, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
+      w.run_of_occ, static_cast<uint32_t>(n), w.scan_status + w.tiles, w.tickets + 9, w.tiles, err,
+      w.run_rank, first_indices_out, unique_out, kUniqueFromValues, values, value_bytes, nullptr,
+      w.run_start, unique_count);
+  FLARE_TRY_HIP(hipGetLastError());
+  inverse_kernel<<<grid, 256, 0, s>>>(w.run_of_occ, w.run_rank, n, inverse_out);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+}  // namespace
+}  // namespace flare
+
+extern "C" int flare_unique_first_occurrence(const void *values, int32_t key_dtype, int64_t n,
+                                             int64_t key_bound, void *unique_out,
+                                             int32_t *inverse_out, int64_t *first_indices_out,
+                                             int64_t *unique_count, void *workspace,
+                                             size_t workspace_bytes, void *stream) {
+  if (n < 0) return fail(FLARE_ERR_SHAPE, "negative key count");
+  if (n > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many keys (%lld)", static_cast<long long>(n));
+  hipStream_t s = as_stream(stream);
+  if (n == 0) {
+    if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
+    return FLARE_OK;
+  }
+  switch (key_dtype) {
+    case FLARE_INT32: return unique_typed(static_cast<const int32_t *>(values), n, key_bound, unique_out, inverse_out, first_indices_out, unique_count, workspace, workspace_bytes, s);
+    case FLARE_UINT32: return unique_typed(static_cast<const uint32_t *>(values), n, key_bound, unique_out, inverse_out, first_indices_out, unique_count, workspace, workspace_bytes, s);
+    case FLARE_INT64: return unique_typed(static_cast<const int64_t *>(values), n, key_bound, unique_out, inverse_out, first_indices_out, unique_count, workspace, workspace_bytes, s);
+    case FLARE_UINT64: return unique_typed(static_cast<const uint64_t *>(values), n, key_bound, unique_out, inverse_out, first_indices_out, unique_count, workspace, workspace_bytes, s);
+    default: return fail(FLARE_ERR_DTYPE, "sparse unique requires integer keys, got dtype code %d", key_dtype);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// sparse_update (store accumulate_gradients + optimizer_step)
+// ----------------------------------------------------------------------------
+extern "C" size_t flare_sparse_update_workspace_bytes(int64_t n, int64_t rows, int32_t dim) {
+  (void)rows;
+  return layout_workspace(nullptr, n, 4, std::max(dim, 1), false, false, true).total_bytes;
+}
+
+extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                   float *state0, float *state1, int32_t *step,
+                                   const flare_optimizer *optimizer, const int64_t *keys, int64_t n,
+                                   const float *grad, int32_t normalization_steps, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
+  if (dim <= 0 || rows < 0 || n < 0) return fail(FLARE_ERR_SHAPE, "invalid sparse update sizes");
+  if (normalization_steps <= 0) return fail(FLARE_ERR_ARGUMENT, "normalization_steps must be a positive integer");
+  if (n > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many keys (%lld)", static_cast<long long>(n));
+  if (rows >= 0xffffffffll) return fail(FLARE_ERR_LIMIT, "too many table rows");
+  int mode = 0;
+  FLARE_TRY(optimizer_mode(optimizer, &mode));
+  if (mode == kModeUnique) return fail(FLARE_ERR_ARGUMENT, "sparse update requires an optimizer (SGD, Adam or row-wise Adagrad)");
+  FLARE_TRY(check_state(mode, state0, state1, step));
+  if (n == 0 || rows == 0) return FLARE_OK;
+  Workspace w = layout_workspace(workspace, n, 4, dim, false, false, true);
+  FLARE_TRY(check_workspace(w, workspace_bytes));
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  hipStream_t s = as_stream(stream);
+  const uint32_t sentinel = static_cast<uint32_t>(rows);
+  const int bits = bits_for(sentinel);
+  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n, 256), 2048));
+  prepare_rows_kernel<int64_t><<<grid, 256, 0, s>>>(keys, n, rows, 0, 0, sort_passes(bits),
+                                                   static_cast<uint32_t *>(w.keys[0]), w.run_of_occ,
+                                                   w.hist, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  return reduce_rows(w, bits, sentinel, err, s, mode, value_dtype, dim, grad, kGradRowOcc, 1,
+                     nullptr, table, state0, state1, step, optimizer, normalization_steps);
+}
+
+// ----------------------------------------------------------------------------
+// pooled_backward (fused scatter_pooled + accumulate + optimizer_step)
+// ----------------------------------------------------------------------------
+extern "C" size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows, int32_t dim) {
+  (void)rows;
+  return layout_workspace(nullptr, n, 4, std::max(dim, 1), true, true, true).total_bytes;
+}
+
+extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                     float *state0, float *state1, int32_t *step,
+                                     const flare_optimizer *optimizer, const void *ids,
+                                     int32_t id_dtype, int64_t n, const int64_t *offsets,
+                                     int32_t num_tables, int64_t batch, const int64_t *row_base,
+                                     int32_t pooling, const float *weights,
+                                     const float *pooled_grad, int32_t normalization_steps,
+                                     float *grad_out, int64_t *unique_out, int32_t *inverse_out,
+                                     int64_t *first_indices_out, int64_t *unique_count,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
+  if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
+    return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
+  if (dim <= 0 || rows < 0 || num_tables <= 0 || batch < 0 || n < 0)
+    return fail(FLARE_ERR_SHAPE, "invalid pooled backward sizes");
+  if (normalization_steps <= 0) return fail(FLARE_ERR_ARGUMENT, "normalization_steps must be a positive integer");
+  if (n > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many occurrences (%lld)", static_cast<long long>(n));
+  if (rows >= 0xffffffffll) return fail(FLARE_ERR_LIMIT, "too many table rows");
+  if (pooling != FLARE_POOL_SUM && pooling != FLARE_POOL_MEAN && pooling != FLARE_POOL_WEIGHTED)
+    return fail(FLARE_ERR_ARGUMENT, "unknown pooling mode %d", pooling);
+  if (pooling == FLARE_POOL_WEIGHTED && !weights)
+    return fail(FLARE_ERR_ARGUMENT, "weighted pooling requires per-sample weights");
+  int mode = 0;
+  FLARE_TRY(optimizer_mode(optimizer, &mode));
+  if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
+  FLARE_TRY(check_state(mode, state0, state1, step));
+  hipStream_t s = as_stream(stream);
+  const int64_t bags = batch * num_tables;
+  if (n == 0 || bags == 0) {
+    if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
+    return FLARE_OK;
+  }
+  const bool need_aux = pooling == FLARE_POOL_MEAN;
+  Workspace w = layout_workspace(workspace, n, 4, dim, true, need_aux, true);
+  FLARE_TRY(check_workspace(w, workspace_bytes));
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  const uint32_t sentinel = static_cast<uint32_t>(rows);
+  const int bits = bits_for(sentinel);
+  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const int pgrid = static_cast<int>(ceil_div(bags, kPrepBags));
+  if (id_dtype == FLARE_INT32)
+    prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
+        static_cast<const int32_t *>(ids), n, offsets, bags, row_base, num_tables, batch, rows,
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, w.aux, w.run_of_occ,
+        w.hist, err);
+  else
+    prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
+        static_cast<const int64_t *>(ids), n, offsets, bags, row_base, num_tables, batch, rows,
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, w.aux, w.run_of_occ,
+        w.hist, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  int sorted = 0;
+  FLARE_TRY(dedup_rows(w, bits, sentinel, err, s, &sorted, first_indices_out, unique_out,
+                       unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count));
+  UpdateArgs a{};
+  a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
+  a.sv = w.vals[sorted];
+  a.run_start = w.run_start;
+  a.unit_first_run = w.unit_first_run;
+  a.meta = w.meta;
+  a.run_rank = w.run_rank;
+  a.inverse_out = inverse_out;
+  a.grad = pooled_grad;
+  a.grad_mode = kGradRowArray;
+  a.grad_row = w.grad_row;
+  a.scale_mode = pooling == FLARE_POOL_WEIGHTED ? kScaleMul : (pooling == FLARE_POOL_MEAN ? kScaleDiv : kScaleNone);
+  a.scale = pooling == FLARE_POOL_WEIGHTED ? weights : w.aux;
+  a.use_norm = normalization_steps != 1;
+  a.norm = static_cast<float>(normalization_steps);
+  a.dim = dim;
+  a.partial = w.partial;
+  a.unit_counter = w.unit_counter;
+  a.out = grad_out;
+  a.table = table;
+  a.s0 = state0;
+  a.s1 = state1;
+  a.step = step;
+  fill_optimizer(a, optimizer);
+  a.units = w.units;
+  a.n = static_cast<uint32_t>(w.n);
+  a.err = err;
+  const bool v4 = vec4_ok(pooled_grad) && (grad_out ? vec4_ok(grad_out) : true) &&
+                  aligned(table, 8) && (mode == kModeAdam ? (vec4_ok(state0) && vec4_ok(state1)) : true) &&
+                  vec4_ok(w.partial);
+  Shape sh;
+  FLARE_TRY(choose_shape(dim, v4, &sh));
+  return launch_update(mode, value_dtype, a, sh, s);
+}

@@ -1,0 +1,54 @@
+// Internal interface of the sort-based dedup / segment-reduce engine.
+#pragma once
+
+#include "common.hpp"
+
+namespace flare {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 occurrences per tile
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+// Sorted positions are reduced in units of kReduceUnit consecutive positions;
+// a key's occurrences inside one unit are summed sequentially and the unit
+// partials of a key that spans several units are folded left to right.
+constexpr int kReduceUnit = 64;
+constexpr uint32_t kInvalidRun = 0x7fffffffu;
+constexpr uint32_t kHeadBit = 0x80000000u;
+constexpr int64_t kMaxOccurrences = (int64_t{1} << 30) - 1;
+
+// Where every array of one call lives inside the caller's workspace.
+struct Workspace {
+  // zero-initialized region (first)
+  uint32_t *hist;         // [8][kRadix] digit histograms, one row per pass
+  uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
+  uint32_t *meta;         // [4]: nvalid, unique count
+  uint32_t *sort_status;  // [8][tiles][kRadix]
+  uint32_t *scan_status;  // [2][tiles]
+  uint32_t *unit_counter; // [units]
+  size_t zero_bytes;
+  // not initialized
+  void *keys[2];
+  uint32_t *vals[2];
+  uint32_t *grad_row;     // [n] (CSR gradient row of each occurrence)
+  float *aux;             // [n] (mean-pooling divisor of each occurrence)
+  uint32_t *run_of_occ;   // [n]
+  uint32_t *run_start;    // [n + 1]
+  uint32_t *run_rank;     // [n]
+  uint32_t *unit_first_run;  // [units]
+  float *partial;         // [units][2][dim]
+  size_t total_bytes;
+  int64_t n;
+  uint32_t tiles;
+  uint32_t units;
+  int key_bytes;
+};
+
+// Computes the layout; with base == nullptr only sizes are filled in.
+Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool need_grad_row,
+                           bool need_aux, bool need_partials);
+
+int bits_for(uint64_t max_value);
+
+}  // namespace flare

@@ -1,0 +1,351 @@
+// Forward kernels: row gather and pooled gather (padded [B,F,M] and CSR).
+//
+// Pooled gather layout on gfx950: a bag is owned by a group of G lanes of one
+// wave64; lane l of the group owns columns [l*VEC, l*VEC+VEC) (+ k*G*VEC),
+// loaded as one 16-byte vector per row (VEC = 8 for fp16/bf16, 4 for fp32),
+// so a D=128 bf16 row is one 256-byte transaction of 16 lanes and a wave
+// pools 4 bags at once.  The block's bag boundaries (CSR offsets) are staged
+// in LDS with one coalesced load; each group then reads its bag's ids G at a
+// time (one per lane, coalesced) and broadcasts them with ds_bpermute.
+// Accumulation is fp32, sequential in occurrence order (the reference's
+// order, gpu_cupy.py:96-103), and rows are loaded four at a time ahead of the
+// adds to keep several 16-byte loads in flight per lane.
+#include "common.hpp"
+
+namespace flare {
+namespace {
+
+constexpr int kThreads = 256;
+
+// ----------------------------------------------------------------------------
+// gather: raw row copy in units of CH bytes (bit-exact, like K1/K3).
+// ----------------------------------------------------------------------------
+template <int CH>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
+    const char *__restrict__ emb, int64_t emb_rows, int64_t row_chunks,
+    const int32_t *__restrict__ inverse, int64_t slots, int32_t pad_index,
+    char *__restrict__ out, int *err) {
+  using R = typename Raw<CH>::type;
+  const int64_t total = slots * row_chunks;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t slot = t / row_chunks;
+    const int64_t c = t - slot * row_chunks;
+    const int32_t row = inverse[slot];
+    R v{};
+    if (row != pad_index) {
+      if (row >= 0 && row < emb_rows) {
+        v = reinterpret_cast<const R *>(emb)[row * row_chunks + c];
+      } else {
+        record_error(err, kErrIndexOutOfRange);
+      }
+    }
+    reinterpret_cast<R *>(out)[t] = v;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// pooled gather
+// ----------------------------------------------------------------------------
+struct PooledArgs {
+  const void *table;
+  int64_t table_rows;
+  int32_t dim;
+  // padded layout: ids = int32 inverse [bags * max_elements]
+  // CSR layout:    ids = IdT [N], offsets int64 [bags + 1]
+  const void *ids;
+  int64_t num_ids;  // CSR: offsets are clamped to [0, num_ids]
+  const int64_t *offsets;
+  const int64_t *row_base;  // CSR: [num_tables + 1]
+  int32_t num_tables;
+  int64_t batch;
+  int32_t max_elements;
+  int32_t pad_index;
+  int32_t pooling;
+  const float *weights;
+  void *out;
+  int64_t bags;
+  int *err;
+};
+
+constexpr int kBagsPerGroup = 4;
+
+template <typename Tag, int VEC, int G, bool kCsr, typename IdT>
+__global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
+  using E = typename Tag::elem;
+  constexpr int kGroups = kThreads / G;
+  constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
+  __shared__ int64_t s_off[kBagsPerBlock + 1];
+
+  const int lane = threadIdx.x % G;
+  const int group = threadIdx.x / G;
+  const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * kBagsPerBlock;
+  const int64_t nbags = (a.bags - bag0) < kBagsPerBlock ? (a.bags - bag0) : kBagsPerBlock;
+
+  if constexpr (kCsr) {
+    for (int i = threadIdx.x; i <= nbags; i += kThreads) {
+      const int64_t o = a.offsets[bag0 + i];
+      s_off[i] = o < 0 ? 0 : (o > a.num_ids ? a.num_ids : o);
+    }
+    __syncthreads();
+  }
+
+  const E *table = static_cast<const E *>(a.table);
+  E *out = static_cast<E *>(a.out);
+  const int D = a.dim;
+
+#pragma unroll 1
+  for (int j = 0; j < kBagsPerGroup; ++j) {
+    const int local = j * kGroups + group;  // consecutive groups take consecutive bags
+    if (local >= nbags) break;
+    const int64_t bag = bag0 + local;
+    int64_t begin, end, row_lo = 0, row_hi = a.table_rows, out_row;
+    if constexpr (kCsr) {
+      begin = s_off[local];
+      end = s_off[local + 1];
+      const int64_t t = bag / a.batch;
+      const int64_t b = bag - t * a.batch;
+      row_lo = a.row_base[t];
+      row_hi = a.row_base[t + 1];
+      out_row = b * a.num_tables + t;
+    } else {
+      begin = bag * a.max_elements;
+      end = begin + a.max_elements;
+      out_row = bag;
+    }
+
+    for (int c0 = 0; c0 < D; c0 += G * VEC) {
+      const int col = c0 + lane * VEC;
+      const bool col_ok = col < D;
+      float acc[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+      int count = 0;
+
+      for (int64_t base = begin; base < end; base += G) {
+        // one id (and weight) per lane, then broadcast inside the group
+        int64_t my_row = -1;
+        float my_w = 1.0f;
+        const int64_t i = base + lane;
+        if (i < end) {
+          const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
+          if constexpr (kCsr) {
+            if (id >= 0 && id < row_hi - row_lo) {
+              my_row = row_lo + id;
+            } else {
+              record_error(a.err, kErrIndexOutOfRange);
+            }
+          } else {
+            if (id != a.pad_index) {
+              if (id >= 0 && id < a.table_rows) {
+                my_row = id;
+              } else {
+                record_error(a.err, kErrIndexOutOfRange);
+              }
+            }
+          }
+          if (a.pooling == FLARE_POOL_WEIGHTED) my_w = a.weights[i];
+        }
+        const int n = (end - base) < G ? static_cast<int>(end - base) : G;
+        for (int k = 0; k < n; k += 4) {
+          int64_t rows[4];
+          float w[4];
+          float x[4][VEC];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int src = (k + u < n) ? (k + u) : 0;
+            rows[u] = __shfl(my_row, src, G);
+            w[u] = __shfl(my_w, src, G);
+            if (k + u >= n) rows[u] = -1;
+            if (rows[u] >= 0 && col_ok) {
+              load_as_f32<Tag, VEC>(table + rows[u] * D + col, x[u]);
+            } else {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) x[u][v] = 0.0f;
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (rows[u] < 0) continue;
+            ++count;
+            if (a.pooling == FLARE_POOL_WEIGHTED) {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[v] += w[u] * x[u][v];
+            } else {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[v] += x[u][v];
+            }
+          }
+        }
+      }
+      if (a.pooling == FLARE_POOL_MEAN) {
+        const float div = static_cast<float>(count > 0 ? count : 1);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = acc[v] / div;
+      }
+      if (col_ok) store_from_f32<Tag, VEC>(out + out_row * D + col, acc);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// host dispatch
+// ----------------------------------------------------------------------------
+int grid_for(int64_t work, int64_t per_block) {
+  const int64_t g = ceil_div(work, per_block);
+  return static_cast<int>(g < 1 ? 1 : (g > 0x7fffffff ? 0x7fffffff : g));
+}
+
+template <typename Tag, int VEC, bool kCsr, typename IdT>
+int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
+  const int64_t per_block = (kThreads / G) * kBagsPerGroup;
+  const int grid = grid_for(a.bags, per_block);
+  switch (G) {
+    case 8: pooled_kernel<Tag, VEC, 8, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 16: pooled_kernel<Tag, VEC, 16, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 32: pooled_kernel<Tag, VEC, 32, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    default: pooled_kernel<Tag, VEC, 64, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+int group_size(int cols) {
+  int g = 8;
+  while (g < cols && g < 64) g <<= 1;
+  return g;
+}
+
+template <typename Tag, bool kCsr, typename IdT>
+int launch_pooled_tag(PooledArgs a, hipStream_t s) {
+  constexpr int kWide = 16 / sizeof(typename Tag::elem);
+  const int esz = sizeof(typename Tag::elem);
+  const bool wide = (a.dim % kWide == 0) && aligned(a.table, 16) && aligned(a.out, 16);
+  if (wide) return launch_pooled_g<Tag, kWide, kCsr, IdT>(a, group_size(a.dim / kWide), s);
+  (void)esz;
+  return launch_pooled_g<Tag, 1, kCsr, IdT>(a, group_size(a.dim), s);
+}
+
+template <bool kCsr, typename IdT>
+int launch_pooled(int dtype, const PooledArgs &a, hipStream_t s) {
+  switch (dtype) {
+    case FLARE_FLOAT32: return launch_pooled_tag<TagF32, kCsr, IdT>(a, s);
+    case FLARE_FLOAT16: return launch_pooled_tag<TagF16, kCsr, IdT>(a, s);
+    case FLARE_BFLOAT16: return launch_pooled_tag<TagBF16, kCsr, IdT>(a, s);
+    default: return fail(FLARE_ERR_DTYPE, "sparse pooled gather requires float16, bfloat16 or float32 embeddings, got dtype code %d", dtype);
+  }
+}
+
+int check_pooling(int pooling, const float *weights) {
+  if (pooling != FLARE_POOL_SUM && pooling != FLARE_POOL_MEAN && pooling != FLARE_POOL_WEIGHTED)
+    return fail(FLARE_ERR_ARGUMENT, "unknown pooling mode %d", pooling);
+  if (pooling == FLARE_POOL_WEIGHTED && !weights)
+    return fail(FLARE_ERR_ARGUMENT, "weighted pooling requires per-sample weights");
+  return FLARE_OK;
+}
+
+}  // namespace
+}  // namespace flare
+
+using namespace flare;
+
+extern "C" int flare_gather(const void *emb, int32_t value_dtype, int64_t emb_rows, int32_t dim,
+                            const int32_t *inverse, int64_t slots, int32_t pad_index, void *out,
+                            void *stream) {
+  const int esz = storage_bytes(value_dtype);
+  if (esz == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse gather requires float16, bfloat16 or float32 embeddings, got dtype code %d", value_dtype);
+  if (dim <= 0 || slots < 0 || emb_rows < 0) return fail(FLARE_ERR_SHAPE, "invalid gather sizes");
+  if (slots == 0) return FLARE_OK;
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  hipStream_t s = as_stream(stream);
+  const int64_t row_bytes = static_cast<int64_t>(dim) * esz;
+  int ch = 2;
+  for (int c : {16, 8, 4}) {
+    if (row_bytes % c == 0 && aligned(emb, c) && aligned(out, c)) { ch = c; break; }
+  }
+  if (ch == 2 && (row_bytes % 2 != 0)) return fail(FLARE_ERR_SHAPE, "row size not a multiple of 2 bytes");
+  const int64_t chunks = row_bytes / ch;
+  const int64_t total = slots * chunks;
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(total, kThreads), 1 << 20));
+  const char *e = static_cast<const char *>(emb);
+  char *o = static_cast<char *>(out);
+  switch (ch) {
+    case 16: gather_rows_kernel<16><<<grid, kThreads, 0, s>>>(e, emb_rows, chunks, inverse, slots, pad_index, o, err); break;
+    case 8: gather_rows_kernel<8><<<grid, kThreads, 0, s>>>(e, emb_rows, chunks, inverse, slots, pad_index, o, err); break;
+    case 4: gather_rows_kernel<4><<<grid, kThreads, 0, s>>>(e, emb_rows, chunks, inverse, slots, pad_index, o, err); break;
+    default: gather_rows_kernel<2><<<grid, kThreads, 0, s>>>(e, emb_rows, chunks, inverse, slots, pad_index, o, err); break;
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+extern "C" int flare_gather_pooled(const void *emb, int32_t value_dtype, int64_t emb_rows,
+                                   int32_t dim, const int32_t *inverse, int64_t batch,
+                                   int32_t features, int32_t max_elements, int32_t pad_index,
+                                   int32_t pooling, const float *weights, void *out,
+                                   void *stream) {
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse pooled gather requires float16, bfloat16 or float32 embeddings, got dtype code %d", value_dtype);
+  if (features <= 0 || max_elements <= 0)
+    return fail(FLARE_ERR_WIDTH, "Sparse embedding pooled operations require positive target widths, got (%d, %d).", features, max_elements);
+  if (dim <= 0 || batch < 0 || emb_rows < 0) return fail(FLARE_ERR_SHAPE, "invalid pooled gather sizes");
+  FLARE_TRY(check_pooling(pooling, weights));
+  const int64_t bags = batch * features;
+  if (bags == 0) return FLARE_OK;
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  PooledArgs a{};
+  a.table = emb;
+  a.table_rows = emb_rows;
+  a.dim = dim;
+  a.ids = inverse;
+  a.max_elements = max_elements;
+  a.pad_index = pad_index;
+  a.pooling = pooling;
+  a.weights = weights;
+  a.out = out;
+  a.bags = bags;
+  a.err = err;
+  return launch_pooled<false, int32_t>(value_dtype, a, as_stream(stream));
+}
+
+extern "C" int flare_gather_pooled_csr(const void *table, int32_t value_dtype, int64_t table_rows,
+                                       int32_t dim, const void *ids, int32_t id_dtype, int64_t n,
+                                       const int64_t *offsets, int32_t num_tables, int64_t batch,
+                                       const int64_t *row_base, int32_t pooling,
+                                       const float *weights, void *out, void *stream) {
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse pooled gather requires float16, bfloat16 or float32 embeddings, got dtype code %d", value_dtype);
+  if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
+    return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
+  if (num_tables <= 0 || batch < 0 || dim <= 0 || table_rows < 0 || n < 0)
+    return fail(FLARE_ERR_SHAPE, "invalid CSR pooled gather sizes");
+  FLARE_TRY(check_pooling(pooling, weights));
+  const int64_t bags = batch * num_tables;
+  if (bags == 0) return FLARE_OK;
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  PooledArgs a{};
+  a.table = table;
+  a.table_rows = table_rows;
+  a.dim = dim;
+  a.ids = ids;
+  a.num_ids = n;
+  a.offsets = offsets;
+  a.row_base = row_base;
+  a.num_tables = num_tables;
+  a.batch = batch;
+  a.pooling = pooling;
+  a.weights = weights;
+  a.out = out;
+  a.bags = bags;
+  a.err = err;
+  hipStream_t s = as_stream(stream);
+  if (id_dtype == FLARE_INT32) return launch_pooled<true, int32_t>(value_dtype, a, s);
+  return launch_pooled<true, int64_t>(value_dtype, a, s);
+}

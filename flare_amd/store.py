@@ -1,0 +1,456 @@
+"""HBM-resident sparse tables and their fused optimizer update.
+
+``EmbeddingStore`` provides the subset of the external ``sparse_embedding``
+store that ``DynamicSparseEmbeddingSPMD`` uses
+(``src/flare/runtime/fluxway/workers/dynamic_embedding.py:251-302,397,525,544``):
+``lookup_or_insert`` / ``lookup`` / ``accumulate_gradients`` /
+``optimizer_step(normalization_steps)`` and their ``async_*`` forms,
+``reserve``, ``value_dtype`` and ``optimizer_dtype``.  Keys are row indices of
+a pre-sized dense shard ``[0, capacity)``; gradients accumulate per key until
+``optimizer_step``, which divides the keyed sum by ``normalization_steps`` and
+applies the optimizer (``dynamic_embedding.py:529-549``).
+
+``PooledTableShard`` packs several tables of one worker into a single HBM
+array and runs the fused hot path: CSR pooled lookup (forward) and
+dedup + segment-reduce + optimizer update straight from pooled gradients
+(backward), i.e. ``gather_pooled`` + ``scatter_pooled`` +
+``accumulate_gradients`` + ``optimizer_step`` without materializing the
+per-key gradients.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+import numpy as np
+import torch
+
+from flare_amd import _native
+from flare_amd.conversion import TORCH_VALUE_DTYPES, contiguous, storage_code, to_device
+from flare_amd.precision import require_sparse_value_dtype
+
+_POOLING = {"sum": _native.POOL_SUM, "mean": _native.POOL_MEAN, "weighted": _native.POOL_WEIGHTED}
+
+
+# ----------------------------------------------------------------------------
+# optimizer and initializer configs (se.Adam / se.Sgd / se.Uniform / se.Zeros)
+# ----------------------------------------------------------------------------
+@dataclass(frozen=True)
+class Adam:
+    """``se.Adam`` (dynamic_embedding.py:89-96); math of audit_sparse_training.py:460-471."""
+
+    lr: float = 0.01
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    weight_decay: float = 0.0
+    dynamic_lr_policy: str = "constant"
+
+
+@dataclass(frozen=True)
+class Sgd:
+    """``se.Sgd`` (dynamic_embedding.py:97-101): ``w -= lr * g``."""
+
+    lr: float = 0.01
+    weight_decay: float = 0.0
+    dynamic_lr_policy: str = "constant"
+
+
+@dataclass(frozen=True)
+class RowWiseAdagrad:
+    """One fp32 accumulator per row: ``acc += mean(g^2); w -= lr*g/(sqrt(acc)+eps)``."""
+
+    lr: float = 0.01
+    eps: float = 1e-8
+    initial_accumulator_value: float = 0.0
+
+
+@dataclass(frozen=True)
+class Uniform:
+    """``se.Uniform`` (the worker's default is ``Uniform(-0.01, 0.01)``, dynamic_embedding.py:263)."""
+
+    min_val: float = -0.01
+    max_val: float = 0.01
+
+
+@dataclass(frozen=True)
+class Zeros:
+    pass
+
+
+def optimizer_from_config(config: Any):
+    """Map a ``SparseOptimizerConfig``-like object (sparse_table/contracts.py:14-25)."""
+    kind = getattr(config, "kind", "adam")
+    policy = getattr(config, "dynamic_lr_policy", "constant")
+    if kind == "adam":
+        return Adam(config.learning_rate, config.beta1, config.beta2, config.eps,
+                    config.weight_decay, policy)
+    if kind == "sgd":
+        return Sgd(config.learning_rate, config.weight_decay, policy)
+    if kind in ("rowwise_adagrad", "adagrad"):
+        return RowWiseAdagrad(config.learning_rate, config.eps)
+    raise ValueError(f"unsupported sparse optimizer {kind!r}")
+
+
+def _native_optimizer(optimizer: Any) -> _native.FlareOptimizer:
+    if getattr(optimizer, "dynamic_lr_policy", "constant") != "constant":
+        raise ValueError(
+            "unsupported sparse dynamic learning-rate policy "
+            f"{optimizer.dynamic_lr_policy!r} (only 'constant' is implemented)"
+        )
+    if getattr(optimizer, "weight_decay", 0.0) != 0.0:
+        raise ValueError("sparse optimizer weight_decay must be 0")
+    o = _native.FlareOptimizer()
+    o.learning_rate = float(optimizer.lr)
+    o.eps = float(getattr(optimizer, "eps", 0.0))
+    o.beta1 = float(getattr(optimizer, "beta1", 0.0))
+    o.beta2 = float(getattr(optimizer, "beta2", 0.0))
+    o.weight_decay = 0.0
+    if isinstance(optimizer, Adam):
+        o.kind = _native.OPT_ADAM
+    elif isinstance(optimizer, Sgd):
+        o.kind = _native.OPT_SGD
+    elif isinstance(optimizer, RowWiseAdagrad):
+        o.kind = _native.OPT_ROWWISE_ADAGRAD
+    elif optimizer is None:
+        o.kind = _native.OPT_NONE
+    else:
+        raise TypeError(f"unsupported sparse optimizer config {type(optimizer).__name__}")
+    return o
+
+
+# ----------------------------------------------------------------------------
+# one dense table with its optimizer state
+# ----------------------------------------------------------------------------
+class _TableState:
+    def __init__(self, rows: int, dim: int, value_dtype: str, optimizer: Any,
+                 initializer: Any, generator: torch.Generator, device: torch.device):
+        self.rows, self.dim = int(rows), int(dim)
+        self.value_dtype = require_sparse_value_dtype(value_dtype)
+        dtype = TORCH_VALUE_DTYPES[value_dtype]
+        if isinstance(initializer, Zeros):
+            table = torch.zeros((self.rows, self.dim), dtype=torch.float32, device=device)
+        else:
+            init = initializer or Uniform()
+            table = torch.empty((self.rows, self.dim), dtype=torch.float32, device=device)
+            table.uniform_(float(init.min_val), float(init.max_val), generator=generator)
+        # fp32 -> storage rounds to nearest even
+        self.table = table.to(dtype)
+        del table
+        self.optimizer = optimizer
+        self.state0 = self.state1 = self.step = None
+        if isinstance(optimizer, Adam):
+            self.state0 = torch.zeros((self.rows, self.dim), dtype=torch.float32, device=device)
+            self.state1 = torch.zeros((self.rows, self.dim), dtype=torch.float32, device=device)
+            self.step = torch.zeros(self.rows, dtype=torch.int32, device=device)
+        elif isinstance(optimizer, RowWiseAdagrad):
+            self.state0 = torch.full((self.rows,), float(optimizer.initial_accumulator_value),
+                                     dtype=torch.float32, device=device)
+        self.native_optimizer = _native_optimizer(optimizer)
+
+    def pointers(self):
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        return p(self.state0), p(self.state1), p(self.step)
+
+
+class _Workspace:
+    """Grow-only device scratch owned by one stream."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.buffer: torch.Tensor | None = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        nbytes = max(int(nbytes), 1)
+        if self.buffer is None or self.buffer.numel() < nbytes:
+            self.buffer = None
+            self.buffer = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self.buffer
+
+
+def _device_of(device: Any) -> torch.device:
+    if device is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    return torch.device(device)
+
+
+# ----------------------------------------------------------------------------
+# EmbeddingStore
+# ----------------------------------------------------------------------------
+class EmbeddingStore:
+    """Dense row-indexed store, one table per embedding dim, resident in HBM."""
+
+    def __init__(self, capacity: int, dims: Sequence[int], *, value_dtype: str = "float32",
+                 optimizer: Any = None, initializer: Any = None, seed: int = 0,
+                 device: Any = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("EmbeddingStore requires a ROCm GPU")
+        _native.library()
+        self.device = _device_of(device)
+        self.capacity = int(capacity)
+        self._value_dtype = require_sparse_value_dtype(value_dtype)
+        self.stream = torch.cuda.Stream(device=self.device)
+        generator = torch.Generator(device=self.device)
+        generator.manual_seed(int(seed))
+        with torch.cuda.stream(self.stream):
+            self.tables = {
+                int(d): _TableState(self.capacity, int(d), value_dtype, optimizer or Adam(),
+                                    initializer, generator, self.device)
+                for d in dims
+            }
+        self._pending: dict[int, list[tuple[torch.Tensor, torch.Tensor]]] = {}
+        self._workspace = _Workspace(self.device)
+
+    # -- metadata -------------------------------------------------------------
+    def value_dtype(self) -> str:
+        return self._value_dtype
+
+    def optimizer_dtype(self) -> str:
+        return "float32"
+
+    def total_size(self) -> int:
+        return self.capacity * len(self.tables)
+
+    def reserve(self, capacity: int, dim: int) -> None:
+        self._table(dim)
+        if int(capacity) > self.capacity:
+            raise ValueError(
+                f"dense sparse shard holds {self.capacity} rows; cannot reserve {capacity}"
+            )
+
+    def contains(self, keys: Any) -> np.ndarray:
+        k = np.asarray(keys, dtype=np.int64)
+        return (k >= 0) & (k < self.capacity)
+
+    def _table(self, dim: int) -> _TableState:
+        try:
+            return self.tables[int(dim)]
+        except KeyError as error:
+            raise ValueError(f"store has no table of dim {dim}") from error
+
+    def _keys(self, keys: Any) -> torch.Tensor:
+        k = to_device(keys, self.device)
+        if k.dtype not in (torch.int64, torch.int32):
+            raise TypeError(f"sparse keys must be int64 (or int32), got {k.dtype}")
+        return contiguous(k.reshape(-1).to(torch.int64))
+
+    # -- lookup ---------------------------------------------------------------
+    def lookup(self, keys: Any, dim: int):
+        """Rows of ``keys`` as a ``[n, dim]`` tensor of the value dtype (DLPack producer)."""
+        table = self._table(dim)
+        with torch.cuda.stream(self.stream):
+            k = self._keys(keys)
+            out = torch.empty((k.numel(), table.dim), dtype=table.table.dtype, device=self.device)
+            if k.numel():
+                inv = contiguous(torch.clamp(k, -1, table.rows).to(torch.int32))
+                _native.call(
+                    "flare_gather", table.table.data_ptr(), storage_code(table.table.dtype),
+                    table.rows, table.dim, inv.data_ptr(), k.numel(), table.rows + 1,
+                    out.data_ptr(), int(self.stream.cuda_stream),
+                )
+        return out, None
+
+    def lookup_or_insert(self, keys: Any, dim: int):
+        """Dense shard: every key in ``[0, capacity)`` already has a row."""
+        return self.lookup(keys, dim)
+
+    # -- update ---------------------------------------------------------------
+    def accumulate_gradients(self, keys: Any, grad: Any) -> None:
+        with torch.cuda.stream(self.stream):
+            k = self._keys(keys)
+            g = to_device(grad, self.device)
+            if g.dtype != torch.float32:
+                g = g.to(torch.float32)
+            if g.dim() != 2 or g.shape[0] != k.numel():
+                raise ValueError(
+                    f"gradient shape {tuple(g.shape)} does not match {k.numel()} keys"
+                )
+            self._table(g.shape[1])
+            self._pending.setdefault(int(g.shape[1]), []).append((k, contiguous(g)))
+
+    def optimizer_step(self, normalization_steps: int) -> None:
+        if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
+            raise ValueError("normalization_steps must be a positive integer")
+        with torch.cuda.stream(self.stream):
+            for dim, items in self._pending.items():
+                table = self._table(dim)
+                keys = items[0][0] if len(items) == 1 else torch.cat([k for k, _ in items])
+                grad = items[0][1] if len(items) == 1 else torch.cat([g for _, g in items])
+                n = int(keys.numel())
+                if n == 0:
+                    continue
+                nbytes = _native.library().flare_sparse_update_workspace_bytes(n, table.rows, table.dim)
+                ws = self._workspace.get(nbytes)
+                s0, s1, st = table.pointers()
+                _native.call(
+                    "flare_sparse_update", table.table.data_ptr(), storage_code(table.table.dtype),
+                    table.rows, table.dim, s0, s1, st, ctypes.byref(table.native_optimizer),
+                    keys.data_ptr(), n, grad.data_ptr(), int(normalization_steps), ws.data_ptr(),
+                    nbytes, int(self.stream.cuda_stream),
+                )
+            self._pending.clear()
+
+    # -- async forms (work is enqueued on the store's stream either way) ------
+    async def async_lookup_or_insert(self, keys: Any, dim: int):
+        return self.lookup_or_insert(keys, dim)
+
+    async def async_lookup(self, keys: Any, dim: int):
+        return self.lookup(keys, dim)
+
+    async def async_accumulate_gradients(self, keys: Any, grad: Any) -> None:
+        self.accumulate_gradients(keys, grad)
+
+    async def async_optimizer_step(self, normalization_steps: int) -> None:
+        self.optimizer_step(normalization_steps)
+
+    def synchronize(self) -> None:
+        self.stream.synchronize()
+
+
+# ----------------------------------------------------------------------------
+# PooledTableShard: the fused forward / backward hot path over T tables
+# ----------------------------------------------------------------------------
+class PooledTableShard:
+    """T tables of one worker packed as ``[sum(rows), dim]`` in HBM.
+
+    Bags are given in CSR form, table-major: for table ``t`` and sample ``b``
+    the bag is ``ids[offsets[t*B + b] : offsets[t*B + b + 1]]`` with
+    table-local row ids.
+    """
+
+    def __init__(self, table_rows: Sequence[int], dim: int, *, value_dtype: str = "bfloat16",
+                 optimizer: Any = None, initializer: Any = None, seed: int = 0,
+                 device: Any = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("PooledTableShard requires a ROCm GPU")
+        _native.library()
+        self.device = _device_of(device)
+        self.table_rows = [int(r) for r in table_rows]
+        self.num_tables = len(self.table_rows)
+        self.dim = int(dim)
+        self.stream = torch.cuda.Stream(device=self.device)
+        base = np.zeros(self.num_tables + 1, dtype=np.int64)
+        base[1:] = np.cumsum(self.table_rows)
+        self.total_rows = int(base[-1])
+        generator = torch.Generator(device=self.device)
+        generator.manual_seed(int(seed))
+        with torch.cuda.stream(self.stream):
+            self.row_base = torch.from_numpy(base).to(self.device)
+            self.state = _TableState(self.total_rows, self.dim, value_dtype,
+                                     optimizer if optimizer is not None else RowWiseAdagrad(),
+                                     initializer, generator, self.device)
+        self._workspace = _Workspace(self.device)
+
+    @property
+    def table(self) -> torch.Tensor:
+        return self.state.table
+
+    def _csr(self, ids: Any, offsets: Any, batch_size: int):
+        ids_t = contiguous(to_device(ids, self.device).reshape(-1))
+        if ids_t.dtype not in (torch.int32, torch.int64):
+            ids_t = ids_t.to(torch.int64)
+        off = contiguous(to_device(offsets, self.device).reshape(-1).to(torch.int64))
+        if off.numel() != self.num_tables * batch_size + 1:
+            raise ValueError(
+                f"offsets must have num_tables * batch_size + 1 = "
+                f"{self.num_tables * batch_size + 1} entries, got {off.numel()}"
+            )
+        return ids_t, off
+
+    def _weights(self, pooling: str, per_sample_weights: Any, n: int):
+        if pooling not in _POOLING:
+            raise ValueError(f"pooling must be one of {sorted(_POOLING)}, got {pooling!r}")
+        if pooling != "weighted":
+            return None
+        if per_sample_weights is None:
+            raise ValueError("weighted pooling requires per_sample_weights")
+        w = contiguous(to_device(per_sample_weights, self.device).reshape(-1).to(torch.float32))
+        if w.numel() != n:
+            raise ValueError("per_sample_weights must have one weight per id")
+        return w
+
+    def lookup_pooled(self, ids: Any, offsets: Any, batch_size: int, *, pooling: str = "sum",
+                      per_sample_weights: Any = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Forward: ``[B, T, D]`` pooled rows in the storage dtype."""
+        with torch.cuda.stream(self.stream):
+            ids_t, off = self._csr(ids, offsets, batch_size)
+            w = self._weights(pooling, per_sample_weights, ids_t.numel())
+            if out is None:
+                out = torch.empty((batch_size, self.num_tables, self.dim),
+                                  dtype=self.state.table.dtype, device=self.device)
+            _native.call(
+                "flare_gather_pooled_csr", self.state.table.data_ptr(),
+                storage_code(self.state.table.dtype), self.total_rows, self.dim,
+                ids_t.data_ptr(), _native.INT32 if ids_t.dtype == torch.int32 else _native.INT64,
+                ids_t.numel(), off.data_ptr(), self.num_tables, batch_size,
+                self.row_base.data_ptr(), _POOLING[pooling], None if w is None else w.data_ptr(),
+                out.data_ptr(),
+                int(self.stream.cuda_stream),
+            )
+        return out
+
+    def _backward(self, ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
+                  normalization_steps, optimizer_override, want_dedup):
+        if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
+            raise ValueError("normalization_steps must be a positive integer")
+        with torch.cuda.stream(self.stream):
+            ids_t, off = self._csr(ids, offsets, batch_size)
+            n = int(ids_t.numel())
+            w = self._weights(pooling, per_sample_weights, n)
+            g = contiguous(to_device(pooled_grad, self.device).to(torch.float32))
+            if g.numel() != batch_size * self.num_tables * self.dim:
+                raise ValueError("pooled gradient must be [batch, num_tables, dim]")
+            opt = optimizer_override if optimizer_override is not None else self.state.native_optimizer
+            grad_out = None
+            if opt.kind == _native.OPT_NONE:
+                grad_out = torch.empty((max(n, 1), self.dim), dtype=torch.float32, device=self.device)
+            unique = inverse = first = count = None
+            if want_dedup or opt.kind == _native.OPT_NONE:
+                unique = torch.empty(max(n, 1), dtype=torch.int64, device=self.device)
+                inverse = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
+                first = torch.empty(max(n, 1), dtype=torch.int64, device=self.device)
+                count = torch.zeros(1, dtype=torch.int64, device=self.device)
+            nbytes = _native.library().flare_pooled_backward_workspace_bytes(n, self.total_rows, self.dim)
+            ws = self._workspace.get(nbytes)
+            s0, s1, st = self.state.pointers()
+            p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+            _native.call(
+                "flare_pooled_backward", self.state.table.data_ptr(),
+                storage_code(self.state.table.dtype), self.total_rows, self.dim, s0, s1, st,
+                ctypes.byref(opt), ids_t.data_ptr(),
+                _native.INT32 if ids_t.dtype == torch.int32 else _native.INT64, n, off.data_ptr(),
+                self.num_tables, batch_size, self.row_base.data_ptr(), _POOLING[pooling], p(w),
+                g.data_ptr(), int(normalization_steps), p(grad_out), p(unique), p(inverse),
+                p(first), p(count), ws.data_ptr(), nbytes, int(self.stream.cuda_stream),
+            )
+        if unique is None:
+            return None
+        u = int(count.item())
+        result = (unique[:u], inverse[:n], first[:u])
+        if grad_out is not None:
+            result = result + (grad_out[:u],)
+        return result
+
+    def apply_pooled_gradients(self, ids: Any, offsets: Any, batch_size: int, pooled_grad: Any, *,
+                               pooling: str = "sum", per_sample_weights: Any = None,
+                               normalization_steps: int = 1, return_dedup: bool = False):
+        """Backward + update: dedup, deterministic segment sum, optimizer on the rows.
+
+        With ``return_dedup`` also returns ``(unique_rows, inverse, first_indices)``
+        (global rows; synchronizes once to read the unique count).
+        """
+        return self._backward(ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
+                              normalization_steps, None, return_dedup)
+
+    def reduce_pooled_gradients(self, ids: Any, offsets: Any, batch_size: int, pooled_grad: Any, *,
+                                pooling: str = "sum", per_sample_weights: Any = None):
+        """Backward only: ``(unique_rows, inverse, first_indices, grads[U, D])``."""
+        none = _native.FlareOptimizer()
+        none.kind = _native.OPT_NONE
+        return self._backward(ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
+                              1, none, True)
+
+    def synchronize(self) -> None:
+        self.stream.synchronize()

@@ -1,0 +1,230 @@
+/*
+ * flare_amd.h -- C ABI of the MI355X (gfx950) sparse-embedding hot path.
+ *
+ * Plain C: device pointers, sizes, enums and a HIP stream handle (passed as
+ * void*).  No torch or other framework types cross this boundary.  Every
+ * function returns 0 (FLARE_OK) or a flare_status code and leaves a message
+ * for flare_last_error().  All work is enqueued asynchronously on the given
+ * stream unless the comment says the call synchronizes.
+ *
+ * Reference interfaces each entry point replaces are cited as path:line in
+ * the fluxway-project/flare tree.
+ */
+#ifndef FLARE_AMD_H
+#define FLARE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLARE_ABI_VERSION 1
+
+/* Status codes; the Python layer maps them to the reference's exception
+ * classes (src/flare/kernels/backends/gpu_cupy.py:351-354,398-401,479-483). */
+typedef enum flare_status {
+  FLARE_OK = 0,
+  FLARE_ERR_DTYPE = 1,     /* unsupported dtype            -> TypeError    */
+  FLARE_ERR_SHAPE = 2,     /* inconsistent sizes           -> ValueError   */
+  FLARE_ERR_WIDTH = 3,     /* bad pooled target widths     -> ValueError   */
+  FLARE_ERR_ARGUMENT = 4,  /* other invalid argument       -> ValueError   */
+  FLARE_ERR_WORKSPACE = 5, /* workspace smaller than asked -> ValueError   */
+  FLARE_ERR_HIP = 6,       /* HIP runtime failure          -> RuntimeError */
+  FLARE_ERR_LIMIT = 7      /* size beyond supported range  -> ValueError   */
+} flare_status;
+
+typedef enum flare_dtype {
+  FLARE_FLOAT32 = 0,
+  FLARE_FLOAT16 = 1,
+  FLARE_BFLOAT16 = 2,
+  FLARE_INT32 = 3,
+  FLARE_INT64 = 4,
+  FLARE_UINT32 = 5,
+  FLARE_UINT64 = 6
+} flare_dtype;
+
+typedef enum flare_pooling {
+  FLARE_POOL_SUM = 0,      /* reference pooling (gpu_cupy.py:96-103)          */
+  FLARE_POOL_MEAN = 1,     /* divisor max(#valid,1), jax/layers/embedding.py:124-126 */
+  FLARE_POOL_WEIGHTED = 2  /* per-sample weights (no reference counterpart)    */
+} flare_pooling;
+
+typedef enum flare_optimizer_kind {
+  FLARE_OPT_NONE = 0,            /* write the deduplicated gradient sum only */
+  FLARE_OPT_SGD = 1,             /* se.Sgd (dynamic_embedding.py:97-101)      */
+  FLARE_OPT_ADAM = 2,            /* se.Adam (dynamic_embedding.py:89-96;
+                                    audit_sparse_training.py:460-471)         */
+  FLARE_OPT_ROWWISE_ADAGRAD = 3  /* one fp32 accumulator per row              */
+} flare_optimizer_kind;
+
+/* Mirrors SparseOptimizerConfig (src/flare/training/components/sparse_table/contracts.py:14-25).
+ * Hyper-parameters are doubles, as the Python config holds them; the kernels
+ * use float32 lr/eps/beta, float32 (1-beta) and float32 bias corrections
+ * 1-beta^step evaluated in double.  weight_decay must be 0 (the only value
+ * whose semantics the reference pins). */
+typedef struct flare_optimizer {
+  int32_t kind;
+  int32_t reserved;
+  double learning_rate;
+  double beta1;
+  double beta2;
+  double eps;
+  double weight_decay;
+} flare_optimizer;
+
+/* Thread-local message of the last failing call on this thread. */
+const char *flare_last_error(void);
+int32_t flare_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Gathers (forward).
+ * ------------------------------------------------------------------------- */
+
+/* SparseEmbeddingOperator.gather (src/flare/kernels/contracts.py:52-61;
+ * CuPy src/flare/kernels/backends/gpu_cupy.py:332-371, kernels :52-73,:108-132).
+ * out[slot,:] = emb[inverse[slot],:], or 0 where inverse[slot] == pad_index.
+ * emb: [emb_rows, dim] of value_dtype (float32/float16/bfloat16); out likewise
+ * [slots, dim].  Slots outside [0, emb_rows) other than pad are written as 0. */
+int flare_gather(const void *emb, int32_t value_dtype, int64_t emb_rows,
+                 int32_t dim, const int32_t *inverse, int64_t slots,
+                 int32_t pad_index, void *out, void *stream);
+
+/* SparseEmbeddingOperator.gather_pooled (contracts.py:63-73; gpu_cupy.py:373-420,
+ * kernels :74-107 fp32 and :133-167 fp16).  inverse: padded [batch, features,
+ * max_elements] int32 with pad_index marking empty slots.  fp32 accumulation in
+ * slot order, output [batch, features, dim] rounded to value_dtype (RNE).
+ * pooling: FLARE_POOL_SUM (reference), _MEAN or _WEIGHTED (weights: float32
+ * [batch, features, max_elements], required only for _WEIGHTED). */
+int flare_gather_pooled(const void *emb, int32_t value_dtype, int64_t emb_rows,
+                        int32_t dim, const int32_t *inverse, int64_t batch,
+                        int32_t features, int32_t max_elements,
+                        int32_t pad_index, int32_t pooling,
+                        const float *weights, void *out, void *stream);
+
+/* CSR pooled gather over num_tables tables packed in one [table_rows, dim]
+ * array: the ragged layout that materialize_padded_inverse
+ * (recipes/recsys/ranking/schema/input.py:23-123) turns into the padded form,
+ * consumed here directly.  Bags are table-major, bag k = t*batch + b, with
+ * occurrences ids[offsets[k] .. offsets[k+1]) (ids int32 or int64, table-local
+ * rows; global row = row_base[t] + id).  row_base: int64 [num_tables + 1],
+ * row_base[num_tables] == table_rows; ids outside [0, row_base[t+1] -
+ * row_base[t]) contribute nothing.  n = number of ids; offsets are clamped
+ * to [0, n] (offsets must start at 0, end at n and not decrease; a violation
+ * sets the device error word).  out: [batch, num_tables, dim]. */
+int flare_gather_pooled_csr(const void *table, int32_t value_dtype,
+                            int64_t table_rows, int32_t dim, const void *ids,
+                            int32_t id_dtype, int64_t n, const int64_t *offsets,
+                            int32_t num_tables, int64_t batch,
+                            const int64_t *row_base, int32_t pooling,
+                            const float *weights, void *out, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Deduplication and gradient reduction (backward).  These need a device
+ * workspace whose size the matching *_workspace_bytes call returns.
+ * Reductions are deterministic: occurrences are stably sorted by key and
+ * summed in occurrence order (no floating-point atomics).
+ * ------------------------------------------------------------------------- */
+
+size_t flare_scatter_workspace_bytes(int64_t slots, int64_t emb_rows, int32_t dim);
+
+/* SparseEmbeddingOperator.scatter (contracts.py:75-84; gpu_cupy.py:422-458,
+ * kernel :168-191).  out[r,:] = sum_{slot: inverse[slot]=r} grad[slot,:];
+ * out: float32 [emb_rows, dim] (fully written, untouched rows are 0). */
+int flare_scatter(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                  int64_t slots, int32_t pad_index, const float *grad,
+                  float *out, void *workspace, size_t workspace_bytes,
+                  void *stream);
+
+/* SparseEmbeddingOperator.scatter_pooled (contracts.py:86-96;
+ * gpu_cupy.py:460-524, kernels :192-252).  grad: float32 [batch, features,
+ * dim]; inverse: [batch, features, max_elements]; slot s takes grad row
+ * s / max_elements.  FLARE_ERR_SHAPE when slots != batch*features*max_elements
+ * (gpu_cupy.py:479-483). */
+int flare_scatter_pooled(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                         int64_t slots, int32_t pad_index, const float *grad,
+                         int64_t batch, int32_t features, int32_t max_elements,
+                         float *out, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
+size_t flare_unique_workspace_bytes(int64_t n, int32_t key_dtype);
+
+/* unique_first_occurrence (src/flare/ops/sparse_unique.py:52-77) and the GPU
+ * dedup branch (src/flare/runtime/fluxway/workers/sparse_input.py:140-164):
+ * unique keys in first-occurrence order, inverse (int32) and first_indices
+ * (int64).  values: [n] of key_dtype (int32/uint32/int64/uint64).
+ * unique_out must hold n keys; *unique_count (device int64) receives U.
+ * key_bound > 0 promises 0 <= key < key_bound (no synchronization); with
+ * key_bound == 0 the call reads the key range back to the host (synchronizes
+ * the stream once). */
+int flare_unique_first_occurrence(const void *values, int32_t key_dtype,
+                                  int64_t n, int64_t key_bound, void *unique_out,
+                                  int32_t *inverse_out,
+                                  int64_t *first_indices_out,
+                                  int64_t *unique_count, void *workspace,
+                                  size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Sparse optimizer update on a dense, row-indexed table shard in HBM.
+ *
+ * table: [rows, dim] value_dtype.  State (float32):
+ *   ROWWISE_ADAGRAD: state0 = accumulator [rows];
+ *   ADAM:            state0 = m [rows, dim], state1 = v [rows, dim],
+ *                    step = int32 per-row counter [rows];
+ *   SGD / NONE:      unused (may be NULL).
+ * ------------------------------------------------------------------------- */
+
+size_t flare_sparse_update_workspace_bytes(int64_t n, int64_t rows, int32_t dim);
+
+/* EmbeddingStore.accumulate_gradients(keys, grad) followed by
+ * optimizer_step(normalization_steps) (dynamic_embedding.py:481-549; store
+ * calls :525,:527,:544,:546).  keys: int64 rows [n] (duplicates allowed; the
+ * gradients of equal keys are summed in occurrence order), grad: float32
+ * [n, dim].  The summed gradient is divided by normalization_steps before the
+ * optimizer.  Keys outside [0, rows) are ignored. */
+int flare_sparse_update(void *table, int32_t value_dtype, int64_t rows,
+                        int32_t dim, float *state0, float *state1,
+                        int32_t *step, const flare_optimizer *optimizer,
+                        const int64_t *keys, int64_t n, const float *grad,
+                        int32_t normalization_steps, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows,
+                                             int32_t dim);
+
+/* Fused backward of flare_gather_pooled_csr: dedup of the occurrence stream
+ * (global row keys row_base[t] + ids[i], i < n == offsets[batch*num_tables]),
+ * per-occurrence gradient
+ * (pooled_grad[b,t,:], times weights[i] for WEIGHTED or / bag length for
+ * MEAN), deterministic segment reduction, then the optimizer update of the
+ * table rows -- scatter_pooled (gpu_cupy.py:460-524) + accumulate_gradients +
+ * optimizer_step fused.  pooled_grad: float32 [batch, num_tables, dim].
+ * With optimizer->kind == FLARE_OPT_NONE the reduced gradient is written to
+ * grad_out [U, dim] in first-occurrence order and the table is not touched.
+ * Optional outputs (NULL to skip): unique_out (int64 global rows, first
+ * occurrence order), inverse_out (int32 [n]), first_indices_out (int64),
+ * unique_count (device int64). */
+int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows,
+                          int32_t dim, float *state0, float *state1,
+                          int32_t *step, const flare_optimizer *optimizer,
+                          const void *ids, int32_t id_dtype, int64_t n,
+                          const int64_t *offsets, int32_t num_tables,
+                          int64_t batch, const int64_t *row_base,
+                          int32_t pooling, const float *weights,
+                          const float *pooled_grad, int32_t normalization_steps,
+                          float *grad_out, int64_t *unique_out,
+                          int32_t *inverse_out, int64_t *first_indices_out,
+                          int64_t *unique_count, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/* Reads back and clears the device-side error word that kernels set when they
+ * meet an out-of-range index (written as 0 / ignored) or an exhausted
+ * spin-wait guard.  Synchronizes the stream.  Returns the flag bits. */
+int32_t flare_take_device_errors(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLARE_AMD_H */

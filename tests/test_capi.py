@@ -1,0 +1,103 @@
+"""The C-ABI library (CPU only: no kernel is launched).
+
+Checks that ``libflare_amd.so`` loads, exports every function that
+``include/flare_amd.h`` declares, and that argument validation, which runs on
+the host before any device work, returns the documented status codes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flare_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "flare_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(flare_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("flare_gather", "flare_gather_pooled", "flare_gather_pooled_csr", "flare_scatter",
+                     "flare_scatter_pooled", "flare_unique_first_occurrence", "flare_sparse_update",
+                     "flare_pooled_backward", "flare_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.library()
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing, missing
+    assert set(_native.SIGNATURES) == set(declared_functions())
+
+
+def test_abi_version_matches_header():
+    version = int(re.search(r"#define FLARE_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert _native.library().flare_abi_version() == version
+
+
+def test_workspace_sizes_are_host_arithmetic():
+    lib = _native.library()
+    small = lib.flare_pooled_backward_workspace_bytes(1000, 10**6, 128)
+    large = lib.flare_pooled_backward_workspace_bytes(1_703_936, 23_000_000, 128)
+    assert 0 < small < large < 256 * 2**20
+    assert lib.flare_unique_workspace_bytes(10, _native.INT64) > 0
+    assert lib.flare_scatter_workspace_bytes(0, 4, 3) > 0
+
+
+def _call(name, *args):
+    return getattr(_native.library(), name)(*args)
+
+
+def test_dtype_errors_map_to_type_error():
+    status = _call("flare_gather", None, 99, 4, 3, None, 4, 4, None, None)
+    assert status == _native.ERR_DTYPE
+    with pytest.raises(TypeError, match="float16, bfloat16 or float32"):
+        _native.check(status)
+    status = _call("flare_unique_first_occurrence", None, _native.FLOAT32, 3, 0, None, None, None,
+                   None, None, 0, None)
+    with pytest.raises(TypeError, match="integer keys"):
+        _native.check(status)
+
+
+def test_width_and_slot_errors_map_to_value_error():
+    status = _call("flare_gather_pooled", None, _native.FLOAT32, 4, 3, None, 4, 0, 2, 4, 0, None, None, None)
+    assert status == _native.ERR_WIDTH
+    with pytest.raises(ValueError, match="positive target widths"):
+        _native.check(status)
+    status = _call("flare_scatter_pooled", 2, 2, None, 3, 2, None, 1, 1, 2, None, None, 0, None)
+    assert status == _native.ERR_SHAPE
+    with pytest.raises(ValueError, match="inverse slots must match"):
+        _native.check(status)
+
+
+def test_optimizer_validation_on_host():
+    opt = _native.FlareOptimizer()
+    opt.kind = _native.OPT_ADAM
+    opt.weight_decay = 0.1
+    status = _call("flare_sparse_update", None, _native.FLOAT32, 10, 4, None, None, None,
+                   ctypes.byref(opt), None, 1, None, 1, None, 0, None)
+    assert status == _native.ERR_ARGUMENT and "weight_decay" in _native.last_error()
+    opt.weight_decay = 0.0
+    status = _call("flare_sparse_update", None, _native.FLOAT32, 10, 4, None, None, None,
+                   ctypes.byref(opt), None, 1, None, 1, None, 0, None)
+    assert status == _native.ERR_ARGUMENT and "Adam requires" in _native.last_error()
+    status = _call("flare_sparse_update", None, _native.FLOAT32, 10, 4, None, None, None,
+                   ctypes.byref(opt), None, 1, None, 0, None, 0, None)
+    assert status == _native.ERR_ARGUMENT and "normalization_steps" in _native.last_error()
+
+
+def test_status_mapping():
+    with pytest.raises(RuntimeError):
+        _native.check(_native.ERR_HIP)
+    for code in (_native.ERR_SHAPE, _native.ERR_WIDTH, _native.ERR_ARGUMENT, _native.ERR_WORKSPACE, _native.ERR_LIMIT):
+        with pytest.raises(ValueError):
+            _native.check(code)
+    _native.check(_native.OK)

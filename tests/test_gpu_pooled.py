@@ -1,0 +1,111 @@
+"""Fused CSR path on the GPU: pooled lookup and pooled-gradient update vs the oracle.
+
+Small-scale versions of the five workloads (same generators, fewer rows and
+samples) are compared against ``oracle.sparse_oracle.pooled_step``:
+pooled outputs bit-exact (same fp32 order, RNE), unique / inverse /
+first_indices bit-exact, optimizer state within rtol 1e-5 and stored rows
+within 1 ulp of the storage dtype.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sparse_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def _shard(w, optimizer, seed=3):
+    from flare_amd.store import Adam, PooledTableShard, RowWiseAdagrad, Sgd, Uniform
+
+    opt = {"rowwise_adagrad": RowWiseAdagrad(lr=0.01, eps=1e-8), "adam": Adam(lr=0.01),
+           "sgd": Sgd(lr=0.01), "none": RowWiseAdagrad()}[optimizer]
+    return PooledTableShard(w.table_rows, w.dim, value_dtype=w.value_dtype, optimizer=opt,
+                            initializer=Uniform(-w.init_range, w.init_range), seed=seed)
+
+
+CASES = [
+    # config, batch, row_scale, optimizer override
+    (1, 512, 0.01, None),
+    (2, 2048, 0.001, None),
+    (3, 256, 0.0005, "rowwise_adagrad"),
+    (4, 1024, 0.0005, None),
+    (5, 256, 0.00005, None),
+    (2, 700, 0.0001, "sgd"),
+    (4, 300, 0.0002, "adam"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_pooled_step_matches_oracle(gpu_device, no_device_errors, case):
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    config, batch, row_scale, override = CASES[case]
+    w = make_workload(config, batch=batch, row_scale=row_scale)
+    optimizer = override or w.optimizer
+    if optimizer == "none":
+        optimizer = "rowwise_adagrad"
+    shard = _shard(w, optimizer)
+    table0 = _host(shard.table.clone())
+    grad = pooled_grad_host(w)
+    pooled = shard.lookup_pooled(w.ids, w.offsets, w.batch, pooling=w.pooling, per_sample_weights=w.weights)
+    dedup = shard.apply_pooled_gradients(w.ids, w.offsets, w.batch, grad, pooling=w.pooling,
+                                         per_sample_weights=w.weights, return_dedup=True)
+    shard.synchronize()
+    state = {}
+    if optimizer == "rowwise_adagrad":
+        state = {"acc": np.zeros(w.total_rows, np.float32)}
+    elif optimizer == "adam":
+        state = {"m": np.zeros((w.total_rows, w.dim), np.float32), "v": np.zeros((w.total_rows, w.dim), np.float32),
+                 "step": np.zeros(w.total_rows, np.int32)}
+    e_pooled, e_table, e_state, e_unique, e_inverse, e_first = O.pooled_step(
+        table0, state, w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad,
+        storage=w.value_dtype, pooling=w.pooling, weights=w.weights, optimizer=optimizer)
+    np.testing.assert_array_equal(_host(pooled), e_pooled)
+    unique, inverse, first = (t.cpu().numpy() for t in dedup)
+    np.testing.assert_array_equal(unique, e_unique)
+    np.testing.assert_array_equal(inverse, e_inverse)
+    np.testing.assert_array_equal(first, e_first)
+    got = _host(shard.table)
+    ulps = O.storage_ulp_distance(got, e_table, w.value_dtype)
+    assert ulps.max() <= 1, f"max ulp {ulps.max()} over {np.count_nonzero(ulps)} elements"
+    if optimizer == "rowwise_adagrad":
+        np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["acc"], rtol=1e-5, atol=0)
+    elif optimizer == "adam":
+        np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["m"], rtol=1e-5, atol=1e-12)
+        np.testing.assert_allclose(shard.state.state1.cpu().numpy(), e_state["v"], rtol=1e-5, atol=1e-15)
+        np.testing.assert_array_equal(shard.state.step.cpu().numpy(), e_state["step"])
+    no_device_errors()
+
+
+@pytest.mark.parametrize("pooling", ["weighted", "mean", "sum"])
+def test_reduced_gradients_bit_exact(gpu_device, no_device_errors, pooling):
+    """Backward-only (workload 3 form): per-key gradients in first-occurrence order."""
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    w = make_workload(3, batch=300, row_scale=0.0002)
+    shard = _shard(w, "rowwise_adagrad")
+    grad = pooled_grad_host(w)
+    pooled = shard.lookup_pooled(w.ids, w.offsets, w.batch, pooling=pooling, per_sample_weights=w.weights)
+    unique, inverse, first, g = shard.reduce_pooled_gradients(w.ids, w.offsets, w.batch, grad, pooling=pooling,
+                                                              per_sample_weights=w.weights)
+    shard.synchronize()
+    eu, ei, ef, eg = O.pooled_grad_sums(w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad,
+                                        pooling=pooling, weights=w.weights)
+    np.testing.assert_array_equal(unique.cpu().numpy(), eu)
+    np.testing.assert_array_equal(inverse.cpu().numpy(), ei)
+    np.testing.assert_array_equal(first.cpu().numpy(), ef)
+    np.testing.assert_array_equal(g.cpu().numpy(), eg)
+    ep = O.gather_pooled_csr(_host(shard.table), w.ids, w.offsets, w.row_base(), w.batch, w.dim,
+                             storage=w.value_dtype, pooling=pooling, weights=w.weights)
+    np.testing.assert_array_equal(_host(pooled), ep)
+    no_device_errors()

@@ -1,0 +1,315 @@
+"""Pins the CPU oracle (CPU only).
+
+Every oracle function is checked against the reference's own known answers
+(cited per test), against an independent formulation, or against what the
+mathematics fixes, so that a plausible slip (dropped term, wrong index,
+transposed operand, wrong rounding) fails here.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sparse_oracle as O
+
+# --------------------------------------------------------------------------- dedup
+
+
+DEDUP_CASES = [  # tests/runtime/test_sparse_input_resources.py:111-117 and :77-105
+    (np.asarray([], np.int64), [], [], []),
+    (np.asarray([7, 7, 7], np.int64), [7], [0, 0, 0], [0]),
+    (np.asarray([3, 1, 3, 2, 1], np.int64), [3, 1, 2], [0, 1, 0, 2, 1], [0, 1, 3]),
+    (np.asarray([-1, 0, -1, np.iinfo(np.int64).min], np.int64),
+     [-1, 0, np.iinfo(np.int64).min], [0, 1, 0, 2], [0, 1, 3]),
+    (np.asarray([2**63, 0, 2**63, 2**64 - 1], np.uint64), [2**63, 0, 2**64 - 1], [0, 1, 0, 2], [0, 1, 3]),
+    (np.asarray([1, 2, 1, 3], np.int64), [1, 2, 3], [0, 1, 0, 2], [0, 1, 3]),
+]
+
+
+@pytest.mark.parametrize("values,unique,inverse,first", DEDUP_CASES)
+@pytest.mark.parametrize("fn", [O.unique_first_occurrence_hash, O.unique_first_occurrence_sorted])
+def test_dedup_known_answers(fn, values, unique, inverse, first):
+    u, i, f = fn(values)
+    assert u.tolist() == unique and i.tolist() == inverse and f.tolist() == first
+    assert i.dtype == np.int32 and f.dtype == np.int64 and u.dtype == values.dtype
+    assert np.array_equal(u[i], values) and np.array_equal(values[f], u)
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_dedup_formulations_agree_and_match_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    values = rng.integers(-50, 50, 2000).astype(np.int64)
+    a = O.unique_first_occurrence_hash(values)
+    b = O.unique_first_occurrence_sorted(values)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    seen: dict[int, int] = {}
+    for v in values.tolist():  # brute force with a dict
+        seen.setdefault(v, len(seen))
+    assert a[0].tolist() == list(seen)
+    assert a[1].tolist() == [seen[v] for v in values.tolist()]
+
+
+def test_dedup_rejects_float_keys():
+    with pytest.raises(TypeError):
+        O.unique_first_occurrence_hash(np.asarray([1.0, 2.0]))
+
+
+# --------------------------------------------------------------------------- gather
+
+
+def test_pooled_gather_known_answer():
+    # tests/kernels/test_sparse_embedding_backend.py:78-89
+    emb = np.arange(8, dtype=np.float32).reshape(4, 2)
+    out = O.gather_pooled(emb, np.asarray([0, 4, 2, 1]), 4, 2, (1, 1), 4)
+    np.testing.assert_array_equal(out.reshape(4, 2), [[0, 1], [0, 0], [4, 5], [2, 3]])
+
+
+def test_fp16_pooled_gather_known_answers():
+    # :162-172, :175-183, :225-233 and the JAX case :144-159
+    e = np.asarray([[1.5, 2.0], [3.0, 4.0]], np.float16)
+    np.testing.assert_array_equal(O.gather_pooled(e, np.asarray([0, 1, 2, 2]), 2, 2, (1, 2), 2, storage="float16"),
+                                  np.asarray([[[4.5, 6.0]], [[0.0, 0.0]]], np.float16))
+    e = np.asarray([[40000.0], [-40000.0], [1.0]], np.float16)
+    np.testing.assert_array_equal(O.gather_pooled(e, np.asarray([0, 1, 2]), 1, 1, (1, 3), 3, storage="float16"),
+                                  np.asarray([[[1.0]]], np.float16))
+    e = np.asarray([[1.5], [2.0]], np.float16)
+    np.testing.assert_array_equal(O.gather_pooled(e, np.asarray([0, 1]), 1, 1, (1, 2), 2, storage="float16"),
+                                  np.asarray([[[3.5]]], np.float16))
+    with np.errstate(over="ignore"):
+        e = np.asarray([[65504.0], [65504.0]], np.float16)
+        assert np.isinf(O.gather_pooled(e, np.asarray([0, 1]), 1, 1, (1, 2), 2, storage="float16")).all()
+
+
+def test_prewarm_probe_shapes():
+    # gpu_cupy.py:539-556: emb arange(12).reshape(4,3), inv [0,4,2,1], pad 4
+    emb = np.arange(12, dtype=np.float32).reshape(4, 3)
+    g = O.gather(emb, np.asarray([0, 4, 2, 1]), 4, 3, 4)
+    assert g.shape == (4, 1, 3)
+    np.testing.assert_array_equal(g.reshape(4, 3), [[0, 1, 2], [0, 0, 0], [6, 7, 8], [3, 4, 5]])
+    s = O.scatter(4, 3, np.asarray([0, 4, 2, 1]), 4, np.ones((4, 3), np.float32))
+    np.testing.assert_array_equal(s, [[1, 1, 1], [1, 1, 1], [1, 1, 1], [0, 0, 0]])
+
+
+def test_pooled_gather_equals_audit_restatement():
+    # tools/validation/audit_sparse_training.py:289-305: padded[inverse].sum(axis=2)
+    rng = np.random.default_rng(0)
+    emb = rng.standard_normal((30, 16)).astype(np.float32)
+    inv = rng.integers(0, 31, (20, 3, 5))
+    padded = np.concatenate([emb, np.zeros((1, 16), np.float32)])
+    ref = padded[inv].sum(axis=2)
+    np.testing.assert_allclose(O.gather_pooled(emb, inv, 20, 16, (3, 5), 30), ref, rtol=2e-6, atol=2e-7)
+
+
+def test_mean_and_weighted_closed_forms():
+    rng = np.random.default_rng(1)
+    emb = rng.standard_normal((10, 4)).astype(np.float32)
+    inv = np.asarray([[[1, 2, 10]], [[10, 10, 10]], [[3, 3, 3]]])
+    w = rng.random(inv.shape).astype(np.float32)
+    mean = O.gather_pooled(emb, inv, 3, 4, (1, 3), 10, pooling="mean")
+    np.testing.assert_allclose(mean[0, 0], (emb[1] + emb[2]) / 2, rtol=1e-6)
+    np.testing.assert_array_equal(mean[1, 0], 0)  # divisor max(0, 1): empty bag stays 0
+    np.testing.assert_allclose(mean[2, 0], emb[3], rtol=1e-6)
+    wsum = O.gather_pooled(emb, inv, 3, 4, (1, 3), 10, pooling="weighted", weights=w)
+    np.testing.assert_allclose(wsum[0, 0], w[0, 0, 0] * emb[1] + w[0, 0, 1] * emb[2], rtol=1e-6)
+    np.testing.assert_allclose(wsum[2, 0], (w[2, 0].sum()) * emb[3], rtol=1e-5)
+
+
+def test_csr_gather_equals_padded_gather():
+    """CSR bags == materialized padded inverse + gather_pooled (schema/input.py:23-123)."""
+    rng = np.random.default_rng(2)
+    rows, dim, batch = 40, 8, 13
+    table = rng.standard_normal((rows, dim)).astype(np.float32)
+    lengths = rng.integers(0, 5, batch)
+    offsets = np.concatenate([[0], np.cumsum(lengths)])
+    ids = rng.integers(0, rows, offsets[-1])
+    csr = O.gather_pooled_csr(table, ids, offsets, np.asarray([0, rows]), batch, dim)
+    padded = O.materialize_padded_inverse_csr(ids, offsets, batch, 4, rows)
+    np.testing.assert_array_equal(csr, O.gather_pooled(table, padded, batch, dim, (1, 4), rows))
+
+
+# --------------------------------------------------------------------------- ragged layout
+
+
+def test_materialize_padded_inverse_reference_vectors():
+    # tests/kernels/test_sparse_cpu_parallel.py:10-31
+    out = O.materialize_padded_inverse(
+        np.asarray([4, 5, 6, 7], np.int32),
+        (np.asarray([0, 2, 4]), np.asarray([0, 1, 3, 3, 4])),
+        pad_index=9, batch_size=2, target_widths=(2, 2))
+    np.testing.assert_array_equal(out, [[[4, 9], [5, 6]], [[9, 9], [7, 9]]])
+    # :74-87 truncation cannot spill into the next row
+    out = O.materialize_padded_inverse(
+        np.asarray([1, 2, 3, 4, 5]), (np.asarray([0, 3, 4]), np.asarray([0, 1, 2, 4, 5])),
+        pad_index=9, batch_size=2, target_widths=(2, 1))
+    np.testing.assert_array_equal(out, [[[1], [2]], [[5], [9]]])
+    # :61-71 offsets outside the flat buffer
+    with pytest.raises(ValueError, match="Invalid ragged inverse offsets"):
+        O.materialize_padded_inverse(np.asarray([1, 2]), (np.asarray([0, 3]),), pad_index=9,
+                                     batch_size=1, target_widths=(3,))
+
+
+# --------------------------------------------------------------------------- scatter
+
+
+def test_scatter_pooled_grouped_reference_case():
+    # tests/kernels/test_sparse_cpu_parallel.py:34-58 (seed 123), Python loop expectation
+    rng = np.random.default_rng(123)
+    emb_rows, batch, fc, me, dim = 17, 1024, 2, 2, 4
+    inverse = rng.integers(0, emb_rows + 1, size=batch * fc * me)
+    inverse[:8] = [1, 1, 2, emb_rows, 3, 1, 2, 2]
+    gradient = rng.standard_normal((batch, fc, dim), dtype=np.float32)
+    actual = O.scatter_pooled(emb_rows, dim, inverse.astype(np.int32), emb_rows, gradient, (fc, me))
+    expected = np.zeros((emb_rows, dim), dtype=np.float32)
+    for slot, row in enumerate(inverse):
+        if row != emb_rows:
+            expected[row] += gradient[slot // (fc * me), (slot // me) % fc]
+    np.testing.assert_allclose(actual, expected, rtol=1e-5, atol=1e-5)
+
+
+def test_scatter_pooled_rejects_partial_slots():
+    with pytest.raises(ValueError, match="inverse slots must match"):
+        O.scatter_pooled(2, 2, np.asarray([0, 1, 2]), 2, np.ones((1, 1, 2), np.float32), (1, 2))
+
+
+def test_segment_sums_single_unit_is_slot_order_bitwise():
+    rng = np.random.default_rng(4)
+    keys = rng.integers(0, 6, 60)  # 60 < REDUCE_UNIT: one unit
+    grads = rng.standard_normal((60, 5)).astype(np.float32)
+    perm, sk, starts = O.sorted_occurrences(keys)
+    sums = O.segment_sums(grads[perm], starts, perm.size)
+    for s, key in enumerate(sk[starts]):
+        acc = np.zeros(5, np.float32)
+        for i in range(60):  # plain slot order, fp32 (sparse_scatter.py:14-32)
+            if keys[i] == key:
+                acc = (acc + grads[i]).astype(np.float32)
+        np.testing.assert_array_equal(sums[s], acc)
+
+
+def test_segment_sums_chunked_order_is_unit_fold():
+    """A key spanning units: sequential inside each unit, partials folded left to right."""
+    unit = 4
+    keys = np.asarray([0, 0, 1, 1, 1, 1, 1, 1, 1, 2])  # key 1 covers positions 2..8
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((10, 3)).astype(np.float32)
+    perm, sk, starts = O.sorted_occurrences(keys)
+    sums = O.segment_sums(g[perm], starts, perm.size, unit=unit)
+    f = np.float32
+    p0 = (g[2] + g[3]).astype(f)                              # unit 0: positions 2, 3
+    p1 = (((g[4] + g[5]).astype(f) + g[6]).astype(f) + g[7]).astype(f)  # unit 1
+    p2 = g[8]                                                 # unit 2
+    np.testing.assert_array_equal(sums[1], ((p0 + p1).astype(f) + p2).astype(f))
+    brute = np.zeros((3, 3), np.float64)
+    np.add.at(brute, keys, g.astype(np.float64))
+    np.testing.assert_allclose(sums, brute, rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------------- optimizers
+
+
+def test_adam_known_answer_two_steps():
+    # tests/runtime/test_sparse_storage_limits.py:41-119: zero init, Adam(lr=0.1), grad 1
+    w = np.zeros((10, 4), np.float32)
+    m = np.zeros_like(w)
+    v = np.zeros_like(w)
+    step = np.zeros(10, np.int32)
+    w, m, v, step = O.adam_update(w, m, v, step, np.ones_like(w), lr=0.1)
+    np.testing.assert_allclose(w, -0.1, rtol=1e-5, atol=1e-6)
+    assert (step == 1).all() and np.all(m != 0) and np.all(v != 0)
+    w, m, v, step = O.adam_update(w, m, v, step, np.ones_like(w), lr=0.1)
+    np.testing.assert_allclose(w, -0.2, rtol=1e-5, atol=1e-6)
+
+
+def test_adam_matches_float64_textbook():
+    rng = np.random.default_rng(6)
+    w = rng.standard_normal((5, 7)).astype(np.float32)
+    g = rng.standard_normal((5, 7)).astype(np.float32)
+    w1, m1, v1, s1 = O.adam_update(w, np.zeros_like(w), np.zeros_like(w), np.zeros(5, np.int32), g, lr=0.01)
+    m = 0.1 * g.astype(np.float64)
+    v = 0.001 * g.astype(np.float64) ** 2
+    ref = w - 0.01 * (m / 0.1) / (np.sqrt(v / 0.001) + 1e-8)
+    np.testing.assert_allclose(w1, ref, rtol=1e-5, atol=1e-7)
+
+
+def test_rowwise_adagrad_reduces_to_optax_for_dim_one():
+    # tests/training/test_optimizer_factories.py:43-51 with initial accumulator 0.1
+    w, acc = O.rowwise_adagrad_update(np.asarray([[1.0]], np.float32), np.asarray([0.1], np.float32),
+                                      np.asarray([[2.0]], np.float32), lr=0.1, eps=1e-8)
+    expected = 1.0 - 0.1 * 2.0 / np.sqrt(0.1 + 2.0**2 + 1e-8)
+    np.testing.assert_allclose(w[0, 0], expected, atol=1e-6)
+    np.testing.assert_allclose(acc[0], 4.1, rtol=1e-7)
+
+
+def test_rowwise_adagrad_uses_row_mean_of_squares():
+    g = np.asarray([[3.0, 4.0]], np.float32)  # mean(g^2) = 12.5
+    w, acc = O.rowwise_adagrad_update(np.zeros((1, 2), np.float32), np.asarray([0.0], np.float32), g, lr=1.0, eps=0.0)
+    np.testing.assert_allclose(acc, [12.5])
+    np.testing.assert_allclose(w, -g / np.sqrt(12.5), rtol=1e-6)
+
+
+def test_sgd_flush_window():
+    # tests/training/test_checkpointing.py:229-251 / :255-298: Sgd(lr=1), zero init, grad [1, 2]
+    np.testing.assert_array_equal(O.sgd_update(np.zeros((1, 2), np.float32), np.asarray([[1.0, 2.0]]), lr=1.0),
+                                  [[-1.0, -2.0]])
+
+
+# --------------------------------------------------------------------------- dtypes
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.standard_normal(10000).astype(np.float32) * np.float32(1e3),
+        np.asarray([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38, 1e-40, 1.00390625, 1.01171875], np.float32),
+        (np.arange(1, 2000, dtype=np.uint32) | np.uint32(0x3F800000)).view(np.float32),
+    ])
+    ours = O.f32_to_bf16_bits(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)
+    np.testing.assert_array_equal(O.bf16_bits_to_f32(ours), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_ulp_distance():
+    a = np.asarray([1.0, -1.0, 0.0], np.float32)
+    b = np.nextafter(a, np.float32(np.inf)).astype(np.float32)
+    assert O.ulp_distance_f32(a, b).tolist() == [1, 1, 1]
+    bb = O.f32_to_bf16_bits(np.asarray([1.0], np.float32))
+    assert O.storage_ulp_distance(bb, bb + 1, "bfloat16").tolist() == [1]
+
+
+# --------------------------------------------------------------------------- fused step
+
+
+def test_pooled_step_equals_composed_reference_ops():
+    """pooled_step == gather_pooled_csr + scatter-by-key + optimizer, composed by hand."""
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    w = make_workload(4, batch=64, row_scale=0.0001)
+    rng = np.random.default_rng(8)
+    table = O.f32_to_storage(rng.uniform(-0.01, 0.01, (w.total_rows, w.dim)).astype(np.float32), "bfloat16")
+    grad = pooled_grad_host(w)
+    state = {"acc": np.zeros(w.total_rows, np.float32)}
+    pooled, new_table, new_state, unique, inverse, first = O.pooled_step(
+        table, state, w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad, storage="bfloat16")
+    keys = w.global_keys()
+    eu, ei, ef = O.unique_first_occurrence_hash(keys)
+    np.testing.assert_array_equal(unique, eu)
+    np.testing.assert_array_equal(inverse, ei)
+    np.testing.assert_array_equal(first, ef)
+    # per-occurrence gradient = the bag's pooled gradient (sum pooling backward)
+    lengths = np.diff(w.offsets)
+    bag = np.repeat(np.arange(w.num_tables * w.batch), lengths)
+    occ_grad = grad[bag % w.batch, bag // w.batch]
+    g = np.zeros((eu.size, w.dim), np.float64)
+    np.add.at(g, ei, occ_grad.astype(np.float64))
+    wt = O.storage_to_f32(table[eu], "bfloat16").astype(np.float64)
+    acc = np.mean(g * g, axis=1)
+    expected = wt - 0.01 * g / (np.sqrt(acc)[:, None] + 1e-8)
+    got = O.storage_to_f32(new_table[eu], "bfloat16")
+    assert O.storage_ulp_distance(new_table[eu], O.f32_to_bf16_bits(expected.astype(np.float32)), "bfloat16").max() <= 1
+    np.testing.assert_allclose(new_state["acc"][eu], acc, rtol=1e-4)
+    untouched = np.setdiff1d(np.arange(w.total_rows), eu)
+    np.testing.assert_array_equal(new_table[untouched], table[untouched])
+    assert got.shape == (eu.size, w.dim) and pooled.shape == (w.batch, w.num_tables, w.dim)
