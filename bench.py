@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused sparse-embedding step on one MI355X.
+
+A step is one pass of the hot path over one batch: CSR pooled lookup
+(forward), id dedup (sort / unique), and the deterministic segment-reduce
+with the row-wise Adagrad update of the table rows (backward).  Default
+workload: 26 tables (rows log-uniform in [1e3, 1e7]), dim 128, bf16 rows with
+fp32 accumulation and fp32 Adagrad state, batch 65536, one id per table per
+sample, Zipf(1.1) ids, synthetic fp32 N(0, 1e-3) pooled gradients.
+
+Inputs are resident in HBM before timing.  Steps rotate over several
+pre-generated id batches so the unique-row footprint exceeds the 256 MB
+Infinity Cache.  HIP events on the shard's stream time each phase; the
+reported step time is the median over the timed steps.
+
+Prints one JSON line (see ``--help``).  ``--gpus`` above 1 is rejected: this
+build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "pooled embedding rows/sec (fwd+bwd+update); achieved HBM GB/s vs 8 TB/s peak"
+PEAK_HBM_GBS = 8000.0
+STATE_BYTES = {"rowwise_adagrad": 4, "sgd": 0}
+WORKLOAD_NAMES = {
+    1: "1 table x 1e6 x 64 fp32, batch 4096, bags U[1,20], Zipf 1.05, row-wise Adagrad",
+    2: "26 tables (rows log-uniform 1e3..1e7) x 128 bf16, batch 65536, bag 1, Zipf 1.1, row-wise Adagrad fp32 state",
+    3: "8 tables x 5e6 x 64 fp16, batch 16384, bags geometric(30)<=500, Zipf 1.05, weighted-sum pooling, backward to reduced grads",
+    4: "26 tables x 2e6 x 128 bf16, batch 65536, bags U[1,8], Zipf 1.3, row-wise Adagrad",
+    5: "1 table x 1e8 x 128 bf16, Adam fp32 m/v, batch 131072, bags U[1,64], Zipf 1.05",
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weighted: bool,
+               optimizer: str) -> tuple[int, int, int]:
+    """Algorithmic HBM bytes (forward, backward, update kernel) of one step.
+
+    forward : ids N*8 + offsets T*(B+1)*4 + weights N*4 + unique rows U*D*s + pooled B*T*D*s
+    backward: ids N*8 + offsets + weights + fp32 pooled grads B*T*D*4 + unique U*8 + inverse N*4
+              + rows 2*U*D*s + state 2*U*S   (S = 4 row-wise Adagrad, 2*D*4+4 Adam)
+              (gradient-only: U*D*4 reduced gradients instead of rows and state)
+    update kernel: grads B*T*D*4 + rows 2*U*D*s + state 2*U*S + inverse N*4
+    """
+    offsets = tables * (batch + 1) * 4
+    w = n * 4 if weighted else 0
+    fwd = n * 8 + offsets + w + u * dim * s + batch * tables * dim * s
+    if optimizer == "none":
+        rows_state = u * dim * 4
+    else:
+        state = 2 * dim * 4 + 4 if optimizer == "adam" else STATE_BYTES[optimizer]
+        rows_state = 2 * u * dim * s + 2 * u * state
+    bwd = n * 8 + offsets + w + batch * tables * dim * 4 + u * 8 + n * 4 + rows_state
+    update = batch * tables * dim * 4 + rows_state + n * 4
+    return fwd, bwd, update
+
+
+def cpu_baseline(config: int, seconds: float) -> dict:
+    """Time the oracle's C restatement of the reference CPU path on host cores."""
+    import numpy as np
+
+    from flare_amd.workload import make_workload
+    from oracle import cpu_step as C
+
+    w = make_workload(config, batch_index=0)
+    storage = w.value_dtype
+    s = {"float32": 4, "float16": 2, "bfloat16": 2}[storage]
+    table = C.init_table(w.total_rows, w.dim, storage, -w.init_range, w.init_range, 11)
+    rng = np.random.default_rng(5)
+    grad = (rng.standard_normal((w.batch, w.num_tables, w.dim), dtype=np.float32) * np.float32(1e-3))
+    opt = w.optimizer
+    if opt == "adam":
+        state = {"m": np.zeros((w.total_rows, w.dim), np.float32), "v": np.zeros((w.total_rows, w.dim), np.float32),
+                 "step": np.zeros(w.total_rows, np.int32)}
+    elif opt == "rowwise_adagrad":
+        state = {"acc": np.zeros(w.total_rows, np.float32)}
+    else:
+        state = {}
+    times = []
+    start = C.now()
+    while (C.now() - start < seconds and len(times) < 50) or len(times) < 3:
+        t0 = C.now()
+        C.pooled_forward(table, storage, w.dim, w.ids, w.offsets, w.num_tables, w.batch, w.row_base(),
+                         w.pooling, w.weights)
+        C.pooled_backward(table, storage, w.dim, state, opt, w.ids, w.offsets, w.num_tables, w.batch,
+                          w.row_base(), grad, w.pooling, w.weights)
+        times.append(C.now() - t0)
+    med = statistics.median(times)
+    return {
+        "value": w.batch * w.num_tables / med,
+        "unit": "pooled rows/s",
+        "cores": C.threads(),
+        "kind": "port",
+        "sample": f"C/OpenMP restatement of the reference Numba path (pooled gather, serial per-table "
+                  f"first-occurrence hash dedup, keyed scatter, optimizer); workload {config} full batch "
+                  f"of {w.batch} x {w.num_tables} bags, median of {len(times)} steps",
+        "ms_per_step": med * 1e3,
+        "storage_bytes": s,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--batches", type=int, default=8, help="pre-generated id batches to rotate over")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only (the tables of one worker's shard on one MI355X); "
+              f"--gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from flare_amd.store import Adam, PooledTableShard, RowWiseAdagrad, Uniform
+    from flare_amd.workload import make_workload
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    config = args.config
+    t_setup = time.time()
+    batches = [make_workload(config, batch_index=k) for k in range(args.batches)]
+    w0 = batches[0]
+    s = {"float32": 4, "float16": 2, "bfloat16": 2}[w0.value_dtype]
+    optimizer = {"rowwise_adagrad": RowWiseAdagrad(lr=0.01, eps=1e-8), "adam": Adam(lr=0.01),
+                 "none": RowWiseAdagrad(lr=0.01, eps=1e-8)}[w0.optimizer]
+    shard = PooledTableShard(w0.table_rows, w0.dim, value_dtype=w0.value_dtype, optimizer=optimizer,
+                             initializer=Uniform(-w0.init_range, w0.init_range), seed=1)
+    plans = [shard.plan_step(b.ids, b.offsets, b.batch, pooling=b.pooling, per_sample_weights=b.weights)
+             for b in batches]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(2)
+    with torch.cuda.stream(shard.stream):
+        grad = torch.randn((w0.batch, w0.num_tables, w0.dim), generator=gen, device=device,
+                           dtype=torch.float32).mul_(1e-3)
+        grad_out = None
+        none_opt = None
+        if w0.optimizer == "none":
+            from flare_amd import _native
+
+            grad_out = torch.empty((max(p.n for p in plans), w0.dim), dtype=torch.float32, device=device)
+            none_opt = _native.FlareOptimizer()
+            none_opt.kind = _native.OPT_NONE
+    # unique counts of every batch (one dedup each, before timing)
+    uniques = []
+    for p in plans:
+        p.dedup()
+    shard.synchronize()
+    for p in plans:
+        uniques.append(int(p.unique_count.item()))
+    log(f"setup {time.time() - t_setup:.1f}s: N={[p.n for p in plans][:3]}..., U={uniques[:3]}...")
+
+    def run(p):
+        p.forward()
+        p.dedup()
+        p.apply(grad, grad_out=grad_out, optimizer=none_opt)
+
+    stream = shard.stream
+    for i in range(args.warmup):
+        run(plans[i % len(plans)])
+    shard.synchronize()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    order = []
+    for i in range(args.steps):
+        k = (args.warmup + i) % len(plans)
+        p = plans[k]
+        order.append(k)
+        ev = events[i]
+        ev[0].record(stream)
+        p.forward()
+        ev[1].record(stream)
+        p.dedup()
+        ev[2].record(stream)
+        p.apply(grad, grad_out=grad_out, optimizer=none_opt)
+        ev[3].record(stream)
+    torch.cuda.synchronize()
+    wall1 = time.perf_counter()
+
+    step_ms, fwd_ms, dedup_ms, apply_ms, gbs, upd_gbs = [], [], [], [], [], []
+    for i, ev in enumerate(events):
+        k = order[i]
+        b = batches[k]
+        f = ev[0].elapsed_time(ev[1])
+        d = ev[1].elapsed_time(ev[2])
+        a = ev[2].elapsed_time(ev[3])
+        t = ev[0].elapsed_time(ev[3])
+        step_ms.append(t)
+        fwd_ms.append(f)
+        dedup_ms.append(d)
+        apply_ms.append(a)
+        fb, bb, ub = step_bytes(b.num_ids, uniques[k], b.batch, b.num_tables, b.dim, s,
+                                b.weights is not None, b.optimizer)
+        gbs.append((fb + bb) / (t * 1e-3) / 1e9)
+        upd_gbs.append(ub / (a * 1e-3) / 1e9)
+    med = statistics.median(step_ms)
+    rows = w0.batch * w0.num_tables
+    achieved_step = statistics.median(gbs)
+    achieved_update = statistics.median(upd_gbs)
+    fb0, bb0, ub0 = step_bytes(w0.num_ids, uniques[0], w0.batch, w0.num_tables, w0.dim, s,
+                               w0.weights is not None, w0.optimizer)
+    result = {
+        "metric": METRIC,
+        "value": rows / (med * 1e-3),
+        "unit": "pooled rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": med,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (bf16 rows)" if w0.value_dtype == "bfloat16" else f"f32 ({w0.value_dtype} rows)",
+        "data": "synthetic (seeded Zipf ids, N(0,1e-3) pooled grads, U(-0.01,0.01) rows)",
+        "config": {
+            "workload": WORKLOAD_NAMES[config],
+            "workload_id": config,
+            "tables": w0.num_tables,
+            "batch": w0.batch,
+            "dim": w0.dim,
+            "ids_per_step": w0.num_ids,
+            "unique_per_step": uniques[0],
+            "rotated_batches": len(plans),
+        },
+        "hbm_gbs": achieved_step,
+        "hbm_frac": achieved_step / PEAK_HBM_GBS,
+        "algorithmic_bytes_per_step": fb0 + bb0,
+        "phases_ms": {
+            "forward_pooled_gather": statistics.median(fwd_ms),
+            "dedup_sort_unique": statistics.median(dedup_ms),
+            "segment_reduce_update": statistics.median(apply_ms),
+        },
+        "wall_ms_per_step": (wall1 - wall0) * 1e3 / args.steps,
+        "roofline": {
+            "kernel": "update_kernel (segment reduce + row-wise update)",
+            "bound": "hbm",
+            "achieved": achieved_update,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": achieved_update / PEAK_HBM_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": ub0,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del plans, grad
+        torch.cuda.empty_cache()
+        try:
+            result["cpu_baseline"] = cpu_baseline(config, args.cpu_seconds)
+        except Exception as error:  # the GPU result stands without the baseline
+            log(f"cpu baseline failed: {error!r}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -61,6 +61,8 @@ SIGNATURES = {
     "flare_sparse_update": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
     "flare_pooled_backward_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "flare_pooled_backward": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_pooled_dedup": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_pooled_apply": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _i64, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "flare_take_device_errors": (_i32, [_vp]),
 }
 

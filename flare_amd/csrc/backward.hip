@@ -45,12 +45,11 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     off = align_up(off + bytes);
     return at;
   };
-  const size_t o_hist = take(8 * kRadix * 4);
+  const size_t o_hist = take(static_cast<size_t>(kHistCopies) * kMaxPasses * kRadix * 4);
   const size_t o_tickets = take(16 * 4);
   const size_t o_meta = take(4 * 4);
   const size_t o_sort_status = take(static_cast<size_t>(8) * w.tiles * kRadix * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
-  const size_t o_unit_counter = take(static_cast<size_t>(w.units) * 4);
   w.zero_bytes = off;
   const size_t o_k0 = take(un * key_bytes);
   const size_t o_k1 = take(un * key_bytes);
@@ -62,6 +61,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_rs = take((un + 1) * 4);
   const size_t o_rr = take(un * 4);
   const size_t o_ufr = take(static_cast<size_t>(w.units) * 4);
+  const size_t o_cross = take(static_cast<size_t>(w.units) * 4);
   const size_t o_part = need_partials ? take(static_cast<size_t>(w.units) * 2 * dim * 4) : 0;
   w.total_bytes = off;
   if (base) {
@@ -71,7 +71,6 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.meta = reinterpret_cast<uint32_t *>(b + o_meta);
     w.sort_status = reinterpret_cast<uint32_t *>(b + o_sort_status);
     w.scan_status = reinterpret_cast<uint32_t *>(b + o_scan_status);
-    w.unit_counter = reinterpret_cast<uint32_t *>(b + o_unit_counter);
     w.keys[0] = b + o_k0;
     w.keys[1] = b + o_k1;
     w.vals[0] = reinterpret_cast<uint32_t *>(b + o_v0);
@@ -82,6 +81,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
     w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
     w.unit_first_run = reinterpret_cast<uint32_t *>(b + o_ufr);
+    w.cross_run = reinterpret_cast<uint32_t *>(b + o_cross);
     w.partial = need_partials ? reinterpret_cast<float *>(b + o_part) : nullptr;
   }
   return w;
@@ -122,10 +122,19 @@ __device__ __forceinline__ void add_histograms(uint32_t *s_hist, K key, int pass
 }
 
 __device__ __forceinline__ void flush_histograms(const uint32_t *s_hist, uint32_t *hist, int passes) {
+  uint32_t *copy = hist + static_cast<size_t>(blockIdx.x % kHistCopies) * kMaxPasses * kRadix;
   for (int i = threadIdx.x; i < passes * kRadix; i += blockDim.x) {
     const uint32_t c = s_hist[i];
-    if (c) atomicAdd(&hist[i], c);
+    if (c) atomicAdd(&copy[i], c);
   }
+}
+
+// Global count of digit d of pass p: sum of the histogram copies.
+__device__ __forceinline__ uint32_t digit_total(const uint32_t *hist, int pass, int d) {
+  uint32_t sum = 0;
+#pragma unroll
+  for (int c = 0; c < kHistCopies; ++c) sum += hist[(static_cast<size_t>(c) * kMaxPasses + pass) * kRadix + d];
+  return sum;
 }
 
 // Keys from a row-index array (int64 store keys or int32 padded inverse).
@@ -163,20 +172,25 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
 // boundaries are staged in LDS; each occurrence finds its bag by binary
 // search there.  Also writes the gradient row (b*T + t) and, for mean
 // pooling, the bag length of every occurrence.
-constexpr int kPrepBags = 256;
+constexpr int kPrepMaxBags = 4096;
+
+// Bags per prepare block: about 2048 blocks, at most kPrepMaxBags bags each.
+int prep_bags_per_block(int64_t bags) {
+  return static_cast<int>(std::min<int64_t>(kPrepMaxBags, std::max<int64_t>(64, ceil_div(bags, 2048))));
+}
 
 template <typename IdT>
 __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
-    const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch, int64_t key_limit,
-    int passes, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
+    int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
+    int64_t key_limit, int passes, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
     float *__restrict__ aux, uint32_t *__restrict__ run_of_occ, uint32_t *__restrict__ hist,
     int *err) {
   __shared__ uint32_t s_hist[4 * kRadix];
-  __shared__ int64_t s_off[kPrepBags + 1];
+  __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
-  const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * kPrepBags;
-  const int nb = static_cast<int>(std::min<int64_t>(kPrepBags, bags - bag0));
+  const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * bags_per_block;
+  const int nb = static_cast<int>(std::min<int64_t>(bags_per_block, bags - bag0));
   for (int i = threadIdx.x; i <= nb; i += 256) {
     const int64_t o = offsets[bag0 + i];
     s_off[i] = o < 0 ? 0 : (o > n ? n : o);
@@ -284,8 +298,9 @@ __global__ void init_minmax_kernel(unsigned long long *out) {
 template <typename K>
 __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const K *__restrict__ kin, const uint32_t *__restrict__ vin, K *__restrict__ kout,
-    uint32_t *__restrict__ vout, uint32_t n, int shift, const uint32_t *__restrict__ hist,
+    uint32_t *__restrict__ vout, uint32_t n, int pass, const uint32_t *__restrict__ hist,
     uint32_t *status, uint32_t *ticket, int *err) {
+  const int shift = pass * kRadixBits;
   __shared__ uint32_t s_tile;
   __shared__ uint32_t s_wcnt[4][kRadix];
   __shared__ uint32_t s_tile_start[kRadix];
@@ -346,7 +361,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
   s_wcnt[2][d] = c0 + c1;
   s_wcnt[3][d] = c0 + c1 + c2;
   const uint32_t tile_start = block_exclusive_scan_256(total, s_scan, nullptr);
-  const uint32_t digit_base = block_exclusive_scan_256(hist[d], s_scan + 4, nullptr);
+  const uint32_t digit_base = block_exclusive_scan_256(digit_total(hist, pass, d), s_scan + 4, nullptr);
   const uint32_t prefix = lookback_exclusive(status, tile, kRadix, d, total, err);
   s_tile_start[d] = tile_start;
   s_gbase[d] = digit_base + prefix;
@@ -568,7 +583,7 @@ struct UpdateArgs {
   float norm;
   int dim;
   float *partial;
-  uint32_t *unit_counter;
+  uint32_t *cross_run;
   float *out;
   void *table;
   float *s0;
@@ -691,6 +706,7 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
   const uint32_t j1 = active ? min(j0 + kReduceUnit, nvalid) : j0;
   const int cnt = static_cast<int>(j1 - j0);
   const int D = a.dim;
+  if (u < a.units && lane == 0) a.cross_run[u] = kNoRun;
 
   // Prefetch occurrence, gradient row and scale of every position of the unit.
   uint32_t occ[kPPL];
@@ -770,9 +786,11 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
     // finish the piece of run r
     const uint32_t seg_start = a.run_start[r];
     const uint32_t seg_end = a.run_start[r + 1];
-    bool do_apply = true;
-    if (!(seg_start >= j0 && seg_end <= j1)) {
-      // the key spans several units: publish this unit's partial
+    if (seg_start >= j0 && seg_end <= j1) {
+      apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
+    } else {
+      // the key spans several units: keep this unit's partial for the fold
+      // (fixup_kernel, after this kernel); slot 1 = the key's first piece
       const int slot = (seg_start < j0) ? 0 : 1;
       float *mine = a.partial + (static_cast<size_t>(u) * 2 + slot) * D;
 #pragma unroll
@@ -780,37 +798,8 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
         const int col = (c * G + lane) * VEC;
         if (col < D) store_f32<VEC>(mine + col, acc[c]);
       }
-      __threadfence();
-      const uint32_t h = seg_start / kReduceUnit;
-      const uint32_t t_unit = (seg_end - 1) / kReduceUnit;
-      uint32_t old = 0;
-      if (lane == 0) old = atomicAdd(&a.unit_counter[h], 1u);
-      old = __shfl(old, 0, G);
-      do_apply = (old == t_unit - h);
-      if (do_apply) {
-        __threadfence();
-        const float *ph = a.partial + (static_cast<size_t>(h) * 2 + 1) * D;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int col = (c * G + lane) * VEC;
-          if (col < D) load_f32<VEC>(ph + col, acc[c]);
-        }
-        for (uint32_t x = h + 1; x <= t_unit; ++x) {
-          const float *px = a.partial + (static_cast<size_t>(x) * 2 + 0) * D;
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const int col = (c * G + lane) * VEC;
-            if (col < D) {
-              float y[VEC];
-              load_f32<VEC>(px + col, y);
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[c][v] += y[v];
-            }
-          }
-        }
-      }
+      if (slot == 1 && lane == 0) a.cross_run[u] = r;
     }
-    if (do_apply) apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
     ++r;
     p = e;
   }
@@ -827,6 +816,65 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
       }
     }
   }
+}
+
+// Fold of keys whose occurrences span several units: the unit holding the
+// key's first piece (slot 1) sums it with the following units' continuation
+// partials (slot 0) left to right, then applies the update once.
+template <typename Tag, int VEC, int G, int NC, int MODE>
+__global__ __launch_bounds__(256) void fixup_kernel(UpdateArgs a) {
+  constexpr int kGroups = 256 / G;
+  const int lane = threadIdx.x % G;
+  const uint32_t u = blockIdx.x * kGroups + threadIdx.x / G;
+  if (u >= a.units) return;
+  const uint32_t r = a.cross_run[u];
+  if (r == kNoRun) return;
+  const int D = a.dim;
+  const uint32_t seg_start = a.run_start[r];
+  const uint32_t seg_end = a.run_start[r + 1];
+  const uint32_t last = (seg_end - 1) / kReduceUnit;
+  float acc[NC][VEC];
+  const float *head = a.partial + (static_cast<size_t>(u) * 2 + 1) * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = (c * G + lane) * VEC;
+    if (col < D) {
+      load_f32<VEC>(head + col, acc[c]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
+    }
+  }
+  uint32_t x = u + 1;
+  for (; x + 4 <= last + 1; x += 4) {  // four partial loads in flight
+    float y[4][NC][VEC];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col < D) load_f32<VEC>(a.partial + (static_cast<size_t>(x + t) * 2) * D + col, y[t][c]);
+      }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[c][v] += y[t][c][v];
+  }
+  for (; x <= last; ++x) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (col < D) {
+        float y[VEC];
+        load_f32<VEC>(a.partial + (static_cast<size_t>(x) * 2) * D + col, y);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[c][v] += y[v];
+      }
+    }
+  }
+  apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -857,20 +905,24 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
+#define FLARE_UPDATE_PAIR(G_, NC_)                                             \
+  update_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);          \
+  fixup_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);
   if (sh.nc == 1) {
     switch (sh.g) {
-      case 8: update_kernel<Tag, VEC, 8, 1, MODE><<<grid(8), 256, 0, s>>>(a); break;
-      case 16: update_kernel<Tag, VEC, 16, 1, MODE><<<grid(16), 256, 0, s>>>(a); break;
-      case 32: update_kernel<Tag, VEC, 32, 1, MODE><<<grid(32), 256, 0, s>>>(a); break;
-      default: update_kernel<Tag, VEC, 64, 1, MODE><<<grid(64), 256, 0, s>>>(a); break;
+      case 8: FLARE_UPDATE_PAIR(8, 1) break;
+      case 16: FLARE_UPDATE_PAIR(16, 1) break;
+      case 32: FLARE_UPDATE_PAIR(32, 1) break;
+      default: FLARE_UPDATE_PAIR(64, 1) break;
     }
   } else {
     switch (sh.nc) {
-      case 2: update_kernel<Tag, VEC, 64, 2, MODE><<<grid(64), 256, 0, s>>>(a); break;
-      case 4: update_kernel<Tag, VEC, 64, 4, MODE><<<grid(64), 256, 0, s>>>(a); break;
-      default: update_kernel<Tag, VEC, 64, 8, MODE><<<grid(64), 256, 0, s>>>(a); break;
+      case 2: FLARE_UPDATE_PAIR(64, 2) break;
+      case 4: FLARE_UPDATE_PAIR(64, 4) break;
+      default: FLARE_UPDATE_PAIR(64, 8) break;
     }
   }
+#undef FLARE_UPDATE_PAIR
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }
@@ -912,8 +964,8 @@ int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result)
   for (int p = 0; p < passes; ++p) {
     onesweep_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
         static_cast<const K *>(w.keys[cur]), p == 0 ? nullptr : w.vals[cur],
-        static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p * kRadixBits,
-        w.hist + p * kRadix, w.sort_status + static_cast<size_t>(p) * w.tiles * kRadix,
+        static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p,
+        w.hist, w.sort_status + static_cast<size_t>(p) * w.tiles * kRadix,
         w.tickets + p, err);
     FLARE_TRY_HIP(hipGetLastError());
     cur ^= 1;
@@ -1006,7 +1058,7 @@ int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipSt
   a.norm = static_cast<float>(norm_steps);
   a.dim = dim;
   a.partial = w.partial;
-  a.unit_counter = w.unit_counter;
+  a.cross_run = w.cross_run;
   a.out = out;
   a.table = table;
   a.s0 = s0;
@@ -1244,41 +1296,39 @@ extern "C" size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows,
   return layout_workspace(nullptr, n, 4, std::max(dim, 1), true, true, true).total_bytes;
 }
 
-extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
-                                     float *state0, float *state1, int32_t *step,
-                                     const flare_optimizer *optimizer, const void *ids,
-                                     int32_t id_dtype, int64_t n, const int64_t *offsets,
-                                     int32_t num_tables, int64_t batch, const int64_t *row_base,
-                                     int32_t pooling, const float *weights,
-                                     const float *pooled_grad, int32_t normalization_steps,
-                                     float *grad_out, int64_t *unique_out, int32_t *inverse_out,
-                                     int64_t *first_indices_out, int64_t *unique_count,
-                                     void *workspace, size_t workspace_bytes, void *stream) {
-  if (storage_bytes(value_dtype) == 0)
-    return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
-  if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
-    return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
+namespace flare {
+namespace {
+int check_pooled_args(int64_t rows, int32_t dim, int32_t num_tables, int64_t batch, int64_t n,
+                      int32_t pooling, const float *weights_if_needed, bool weights_required) {
   if (dim <= 0 || rows < 0 || num_tables <= 0 || batch < 0 || n < 0)
     return fail(FLARE_ERR_SHAPE, "invalid pooled backward sizes");
-  if (normalization_steps <= 0) return fail(FLARE_ERR_ARGUMENT, "normalization_steps must be a positive integer");
   if (n > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many occurrences (%lld)", static_cast<long long>(n));
   if (rows >= 0xffffffffll) return fail(FLARE_ERR_LIMIT, "too many table rows");
   if (pooling != FLARE_POOL_SUM && pooling != FLARE_POOL_MEAN && pooling != FLARE_POOL_WEIGHTED)
     return fail(FLARE_ERR_ARGUMENT, "unknown pooling mode %d", pooling);
-  if (pooling == FLARE_POOL_WEIGHTED && !weights)
+  if (weights_required && pooling == FLARE_POOL_WEIGHTED && !weights_if_needed)
     return fail(FLARE_ERR_ARGUMENT, "weighted pooling requires per-sample weights");
-  int mode = 0;
-  FLARE_TRY(optimizer_mode(optimizer, &mode));
-  if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
-  FLARE_TRY(check_state(mode, state0, state1, step));
+  return FLARE_OK;
+}
+}  // namespace
+}  // namespace flare
+
+extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
+                                  const int64_t *offsets, int32_t num_tables, int64_t batch,
+                                  const int64_t *row_base, int64_t rows, int32_t dim,
+                                  int32_t pooling, int64_t *unique_out,
+                                  int64_t *first_indices_out, int64_t *unique_count,
+                                  void *workspace, size_t workspace_bytes, void *stream) {
+  if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
+    return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
+  FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, nullptr, false));
   hipStream_t s = as_stream(stream);
   const int64_t bags = batch * num_tables;
   if (n == 0 || bags == 0) {
     if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
     return FLARE_OK;
   }
-  const bool need_aux = pooling == FLARE_POOL_MEAN;
-  Workspace w = layout_workspace(workspace, n, 4, dim, true, need_aux, true);
+  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
   int *err = device_error_word(&st);
@@ -1286,21 +1336,49 @@ extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t r
   const uint32_t sentinel = static_cast<uint32_t>(rows);
   const int bits = bits_for(sentinel);
   FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
-  const int pgrid = static_cast<int>(ceil_div(bags, kPrepBags));
+  const int bpb = prep_bags_per_block(bags);
+  const int pgrid = static_cast<int>(ceil_div(bags, bpb));
+  float *aux = pooling == FLARE_POOL_MEAN ? w.aux : nullptr;
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
-        static_cast<const int32_t *>(ids), n, offsets, bags, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, w.aux, w.run_of_occ,
+        static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.run_of_occ,
         w.hist, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
-        static_cast<const int64_t *>(ids), n, offsets, bags, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, w.aux, w.run_of_occ,
+        static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.run_of_occ,
         w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
-  FLARE_TRY(dedup_rows(w, bits, sentinel, err, s, &sorted, first_indices_out, unique_out,
-                       unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count));
+  return dedup_rows(w, bits, sentinel, err, s, &sorted, first_indices_out, unique_out,
+                    unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count);
+}
+
+extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                  float *state0, float *state1, int32_t *step,
+                                  const flare_optimizer *optimizer, int64_t n,
+                                  int32_t num_tables, int64_t batch, int32_t pooling,
+                                  const float *weights, const float *pooled_grad,
+                                  int32_t normalization_steps, float *grad_out,
+                                  int32_t *inverse_out, void *workspace, size_t workspace_bytes,
+                                  void *stream) {
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
+  FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, weights, true));
+  if (normalization_steps <= 0) return fail(FLARE_ERR_ARGUMENT, "normalization_steps must be a positive integer");
+  int mode = 0;
+  FLARE_TRY(optimizer_mode(optimizer, &mode));
+  if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
+  FLARE_TRY(check_state(mode, state0, state1, step));
+  if (n == 0 || batch * num_tables == 0) return FLARE_OK;
+  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true);
+  FLARE_TRY(check_workspace(w, workspace_bytes));
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  const int bits = bits_for(static_cast<uint32_t>(rows));
+  const int sorted = sort_passes(bits) & 1;  // buffer holding the sorted pairs
   UpdateArgs a{};
   a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
   a.sv = w.vals[sorted];
@@ -1318,7 +1396,7 @@ extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t r
   a.norm = static_cast<float>(normalization_steps);
   a.dim = dim;
   a.partial = w.partial;
-  a.unit_counter = w.unit_counter;
+  a.cross_run = w.cross_run;
   a.out = grad_out;
   a.table = table;
   a.s0 = state0;
@@ -1333,5 +1411,32 @@ extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t r
                   vec4_ok(w.partial);
   Shape sh;
   FLARE_TRY(choose_shape(dim, v4, &sh));
-  return launch_update(mode, value_dtype, a, sh, s);
+  return launch_update(mode, value_dtype, a, sh, as_stream(stream));
+}
+
+extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                     float *state0, float *state1, int32_t *step,
+                                     const flare_optimizer *optimizer, const void *ids,
+                                     int32_t id_dtype, int64_t n, const int64_t *offsets,
+                                     int32_t num_tables, int64_t batch, const int64_t *row_base,
+                                     int32_t pooling, const float *weights,
+                                     const float *pooled_grad, int32_t normalization_steps,
+                                     float *grad_out, int64_t *unique_out, int32_t *inverse_out,
+                                     int64_t *first_indices_out, int64_t *unique_count,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  // validate everything before enqueuing any work
+  if (storage_bytes(value_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
+  FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, weights, true));
+  if (normalization_steps <= 0) return fail(FLARE_ERR_ARGUMENT, "normalization_steps must be a positive integer");
+  int mode = 0;
+  FLARE_TRY(optimizer_mode(optimizer, &mode));
+  if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
+  FLARE_TRY(check_state(mode, state0, state1, step));
+  FLARE_TRY(flare_pooled_dedup(ids, id_dtype, n, offsets, num_tables, batch, row_base, rows, dim,
+                               pooling, unique_out, first_indices_out, unique_count, workspace,
+                               workspace_bytes, stream));
+  return flare_pooled_apply(table, value_dtype, rows, dim, state0, state1, step, optimizer, n,
+                            num_tables, batch, pooling, weights, pooled_grad, normalization_steps,
+                            grad_out, inverse_out, workspace, workspace_bytes, stream);
 }

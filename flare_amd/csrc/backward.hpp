@@ -17,16 +17,20 @@ constexpr int kReduceUnit = 64;
 constexpr uint32_t kInvalidRun = 0x7fffffffu;
 constexpr uint32_t kHeadBit = 0x80000000u;
 constexpr int64_t kMaxOccurrences = (int64_t{1} << 30) - 1;
+// Blocks add their digit histograms into one of kHistCopies copies (by block
+// index) to spread same-address atomics; a radix pass sums the copies.
+constexpr int kHistCopies = 16;
+constexpr int kMaxPasses = 8;
+constexpr uint32_t kNoRun = 0xffffffffu;
 
 // Where every array of one call lives inside the caller's workspace.
 struct Workspace {
   // zero-initialized region (first)
-  uint32_t *hist;         // [8][kRadix] digit histograms, one row per pass
+  uint32_t *hist;         // [kHistCopies][kMaxPasses][kRadix] digit histograms
   uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
   uint32_t *meta;         // [4]: nvalid, unique count
   uint32_t *sort_status;  // [8][tiles][kRadix]
   uint32_t *scan_status;  // [2][tiles]
-  uint32_t *unit_counter; // [units]
   size_t zero_bytes;
   // not initialized
   void *keys[2];
@@ -37,6 +41,7 @@ struct Workspace {
   uint32_t *run_start;    // [n + 1]
   uint32_t *run_rank;     // [n]
   uint32_t *unit_first_run;  // [units]
+  uint32_t *cross_run;    // [units] run whose head piece this unit holds, or kNoRun
   float *partial;         // [units][2][dim]
   size_t total_bytes;
   int64_t n;

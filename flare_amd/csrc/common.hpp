@@ -174,11 +174,15 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
 //
 // status[tile * stride + idx] holds a 2-bit flag and a 30-bit count:
 //   flag 1 = this tile's own aggregate, flag 2 = inclusive prefix.
-// Tiles are numbered in the order they start (atomic ticket), so a tile only
-// waits for tiles that are already running and publish their aggregate
-// before waiting themselves: the wait always ends.  The spin count is still
-// bounded; if the guard trips, the error word gets kErrSpinGuard and callers
-// clamp every write to stay inside their buffers.
+// The count travels inside the status word, so the words are written and
+// read with relaxed agent-scope atomics, which bypass the per-XCD L2 and need
+// no fence.  (On gfx942/gfx950 an agent-scope release or acquire writes back
+// or invalidates the XCD's L2; issuing one per status word serializes the
+// whole scan.)  Tiles are numbered in the order they start (atomic ticket),
+// so a tile only waits for tiles that are already running and publish their
+// aggregate before waiting themselves: the wait always ends.  The spin count
+// is still bounded; if the guard trips, the error word gets kErrSpinGuard and
+// callers clamp every write to stay inside their buffers.
 // ----------------------------------------------------------------------------
 constexpr uint32_t kFlagAggregate = 1u << 30;
 constexpr uint32_t kFlagPrefix = 2u << 30;
@@ -186,7 +190,11 @@ constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kSpinLimit = 1u << 22;
 
 __device__ __forceinline__ void publish(uint32_t *p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t peek(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_t tile,
@@ -202,8 +210,7 @@ __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_
   int64_t t = static_cast<int64_t>(tile) - 1;
   uint32_t spins = 0;
   while (t >= 0) {
-    const uint32_t s = __hip_atomic_load(status + static_cast<size_t>(t) * stride + idx,
-                                         __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t s = peek(status + static_cast<size_t>(t) * stride + idx);
     const uint32_t flag = s & ~kCountMask;
     if (flag == 0) {
       if (++spins > kSpinLimit) {

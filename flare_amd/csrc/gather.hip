@@ -75,6 +75,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   using E = typename Tag::elem;
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
+  constexpr int B4 = kBagsPerGroup;
   __shared__ int64_t s_off[kBagsPerBlock + 1];
 
   const int lane = threadIdx.x % G;
@@ -93,97 +94,125 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   const E *table = static_cast<const E *>(a.table);
   E *out = static_cast<E *>(a.out);
   const int D = a.dim;
+  const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
 
-#pragma unroll 1
-  for (int j = 0; j < kBagsPerGroup; ++j) {
-    const int local = j * kGroups + group;  // consecutive groups take consecutive bags
-    if (local >= nbags) break;
-    const int64_t bag = bag0 + local;
-    int64_t begin, end, row_lo = 0, row_hi = a.table_rows, out_row;
-    if constexpr (kCsr) {
-      begin = s_off[local];
-      end = s_off[local + 1];
-      const int64_t t = bag / a.batch;
-      const int64_t b = bag - t * a.batch;
-      row_lo = a.row_base[t];
-      row_hi = a.row_base[t + 1];
-      out_row = b * a.num_tables + t;
-    } else {
-      begin = bag * a.max_elements;
-      end = begin + a.max_elements;
-      out_row = bag;
-    }
-
-    for (int c0 = 0; c0 < D; c0 += G * VEC) {
-      const int col = c0 + lane * VEC;
-      const bool col_ok = col < D;
-      float acc[VEC];
+  // The group's bags (consecutive groups take consecutive bags).
+  int64_t begin[B4], len[B4], row_lo[B4], row_hi[B4], out_row[B4];
+  int64_t max_len = 0;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-      int count = 0;
+  for (int j = 0; j < B4; ++j) {
+    const int local = j * kGroups + group;
+    begin[j] = 0;
+    len[j] = 0;
+    row_lo[j] = 0;
+    row_hi[j] = a.table_rows;
+    out_row[j] = -1;
+    if (local < nbags) {
+      const int64_t bag = bag0 + local;
+      if constexpr (kCsr) {
+        begin[j] = s_off[local];
+        len[j] = s_off[local + 1] - begin[j];
+        if (len[j] < 0) len[j] = 0;
+        const int64_t t = bag / a.batch;
+        const int64_t b = bag - t * a.batch;
+        row_lo[j] = a.row_base[t];
+        row_hi[j] = a.row_base[t + 1];
+        out_row[j] = b * a.num_tables + t;
+      } else {
+        begin[j] = bag * a.max_elements;
+        len[j] = a.max_elements;
+        out_row[j] = bag;
+      }
+      max_len = len[j] > max_len ? len[j] : max_len;
+    }
+  }
 
-      for (int64_t base = begin; base < end; base += G) {
-        // one id (and weight) per lane, then broadcast inside the group
-        int64_t my_row = -1;
-        float my_w = 1.0f;
-        const int64_t i = base + lane;
-        if (i < end) {
+  for (int c0 = 0; c0 < D; c0 += G * VEC) {
+    const int col = c0 + lane * VEC;
+    const bool col_ok = col < D;
+    float acc[B4][VEC];
+    int count[B4];
+#pragma unroll
+    for (int j = 0; j < B4; ++j) {
+      count[j] = 0;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[j][v] = 0.0f;
+    }
+    for (int64_t k0 = 0; k0 < max_len; k0 += G) {
+      // one id (and weight) per lane for each of the four bags
+      int64_t my_row[B4];
+      float my_w[B4];
+#pragma unroll
+      for (int j = 0; j < B4; ++j) {
+        my_row[j] = -1;
+        my_w[j] = 1.0f;
+        const int64_t e = k0 + lane;
+        if (e < len[j]) {
+          const int64_t i = begin[j] + e;
           const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
           if constexpr (kCsr) {
-            if (id >= 0 && id < row_hi - row_lo) {
-              my_row = row_lo + id;
+            if (id >= 0 && id < row_hi[j] - row_lo[j]) {
+              my_row[j] = row_lo[j] + id;
             } else {
               record_error(a.err, kErrIndexOutOfRange);
             }
-          } else {
-            if (id != a.pad_index) {
-              if (id >= 0 && id < a.table_rows) {
-                my_row = id;
-              } else {
-                record_error(a.err, kErrIndexOutOfRange);
-              }
-            }
-          }
-          if (a.pooling == FLARE_POOL_WEIGHTED) my_w = a.weights[i];
-        }
-        const int n = (end - base) < G ? static_cast<int>(end - base) : G;
-        for (int k = 0; k < n; k += 4) {
-          int64_t rows[4];
-          float w[4];
-          float x[4][VEC];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int src = (k + u < n) ? (k + u) : 0;
-            rows[u] = __shfl(my_row, src, G);
-            w[u] = __shfl(my_w, src, G);
-            if (k + u >= n) rows[u] = -1;
-            if (rows[u] >= 0 && col_ok) {
-              load_as_f32<Tag, VEC>(table + rows[u] * D + col, x[u]);
+          } else if (id != a.pad_index) {
+            if (id >= 0 && id < a.table_rows) {
+              my_row[j] = id;
             } else {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) x[u][v] = 0.0f;
+              record_error(a.err, kErrIndexOutOfRange);
             }
           }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (rows[u] < 0) continue;
-            ++count;
-            if (a.pooling == FLARE_POOL_WEIGHTED) {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[v] += w[u] * x[u][v];
-            } else {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[v] += x[u][v];
-            }
-          }
+          if (weighted) my_w[j] = a.weights[i];
         }
       }
+      const int64_t remain = max_len - k0;
+      const int n = remain < G ? static_cast<int>(remain) : G;
+      for (int k = 0; k < n; k += 2) {
+        // two elements of each of the four bags: eight row loads in flight
+        int64_t rows[2][B4];
+        float w[2][B4];
+        float x[2][B4][VEC];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < B4; ++j) {
+            const int src = (k + h < n) ? (k + h) : 0;
+            rows[h][j] = __shfl(my_row[j], src, G);
+            w[h][j] = __shfl(my_w[j], src, G);
+            if (k + h >= n) rows[h][j] = -1;
+            if (rows[h][j] >= 0 && col_ok) {
+              load_as_f32<Tag, VEC>(table + rows[h][j] * D + col, x[h][j]);
+            } else {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) x[h][j][v] = 0.0f;
+            }
+          }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < B4; ++j) {
+            if (rows[h][j] < 0) continue;
+            ++count[j];
+            if (weighted) {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[j][v] += w[h][j] * x[h][j][v];
+            } else {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) acc[j][v] += x[h][j][v];
+            }
+          }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < B4; ++j) {
+      if (out_row[j] < 0) continue;
       if (a.pooling == FLARE_POOL_MEAN) {
-        const float div = static_cast<float>(count > 0 ? count : 1);
+        const float div = static_cast<float>(count[j] > 0 ? count[j] : 1);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[v] = acc[v] / div;
+        for (int v = 0; v < VEC; ++v) acc[j][v] = acc[j][v] / div;
       }
-      if (col_ok) store_from_f32<Tag, VEC>(out + out_row * D + col, acc);
+      if (col_ok) store_from_f32<Tag, VEC>(out + out_row[j] * D + col, acc[j]);
     }
   }
 }

@@ -427,6 +427,7 @@ class PooledTableShard:
             )
         if unique is None:
             return None
+        self.stream.synchronize()  # the count is read on the host
         u = int(count.item())
         result = (unique[:u], inverse[:n], first[:u])
         if grad_out is not None:
@@ -452,5 +453,81 @@ class PooledTableShard:
         return self._backward(ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
                               1, none, True)
 
+    def plan_step(self, ids: Any, offsets: Any, batch_size: int, *, pooling: str = "sum",
+                  per_sample_weights: Any = None) -> "PooledStepPlan":
+        """Bind one batch's device buffers for allocation-free forward / dedup / apply."""
+        return PooledStepPlan(self, ids, offsets, batch_size, pooling, per_sample_weights)
+
     def synchronize(self) -> None:
         self.stream.synchronize()
+
+
+class PooledStepPlan:
+    """One batch of a ``PooledTableShard``, with every buffer allocated up front.
+
+    ``forward()`` pools into ``self.pooled``; ``dedup()`` sorts the ids and
+    writes ``unique`` / ``first_indices`` / ``unique_count`` (device);
+    ``apply(pooled_grad)`` reduces the gradient, updates the rows and writes
+    ``inverse``.  No call allocates or synchronizes, so a loop of steps stays
+    asynchronous on the shard's stream.
+    """
+
+    def __init__(self, shard: PooledTableShard, ids: Any, offsets: Any, batch_size: int,
+                 pooling: str, per_sample_weights: Any):
+        self.shard = shard
+        self.batch = int(batch_size)
+        self.pooling = pooling
+        dev = shard.device
+        with torch.cuda.stream(shard.stream):
+            self.ids, self.offsets = shard._csr(ids, offsets, self.batch)
+            self.n = int(self.ids.numel())
+            self.weights = shard._weights(pooling, per_sample_weights, self.n)
+            self.pooled = torch.empty((self.batch, shard.num_tables, shard.dim),
+                                      dtype=shard.state.table.dtype, device=dev)
+            m = max(self.n, 1)
+            self.unique = torch.empty(m, dtype=torch.int64, device=dev)
+            self.first_indices = torch.empty(m, dtype=torch.int64, device=dev)
+            self.inverse = torch.empty(m, dtype=torch.int32, device=dev)
+            self.unique_count = torch.zeros(1, dtype=torch.int64, device=dev)
+            self.workspace_bytes = _native.library().flare_pooled_backward_workspace_bytes(
+                self.n, shard.total_rows, shard.dim)
+            self.workspace = torch.empty(max(self.workspace_bytes, 1), dtype=torch.uint8, device=dev)
+        self._id_code = _native.INT32 if self.ids.dtype == torch.int32 else _native.INT64
+        self._stream = int(shard.stream.cuda_stream)
+
+    def forward(self) -> torch.Tensor:
+        s = self.shard
+        _native.call(
+            "flare_gather_pooled_csr", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
+            s.total_rows, s.dim, self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
+            s.num_tables, self.batch, s.row_base.data_ptr(), _POOLING[self.pooling],
+            None if self.weights is None else self.weights.data_ptr(), self.pooled.data_ptr(),
+            self._stream,
+        )
+        return self.pooled
+
+    def dedup(self) -> None:
+        s = self.shard
+        _native.call(
+            "flare_pooled_dedup", self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
+            s.num_tables, self.batch, s.row_base.data_ptr(), s.total_rows, s.dim,
+            _POOLING[self.pooling], self.unique.data_ptr(), self.first_indices.data_ptr(),
+            self.unique_count.data_ptr(), self.workspace.data_ptr(), self.workspace_bytes, self._stream,
+        )
+
+    def apply(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
+              grad_out: torch.Tensor | None = None, optimizer: Any = None) -> None:
+        s = self.shard
+        if pooled_grad.dtype != torch.float32 or not pooled_grad.is_contiguous() or \
+                pooled_grad.numel() != self.batch * s.num_tables * s.dim or pooled_grad.device != s.device:
+            raise ValueError("pooled_grad must be a contiguous float32 [batch, num_tables, dim] device tensor")
+        opt = s.state.native_optimizer if optimizer is None else optimizer
+        s0, s1, st = s.state.pointers()
+        _native.call(
+            "flare_pooled_apply", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
+            s.total_rows, s.dim, s0, s1, st, ctypes.byref(opt), self.n, s.num_tables, self.batch,
+            _POOLING[self.pooling], None if self.weights is None else self.weights.data_ptr(),
+            pooled_grad.data_ptr(), int(normalization_steps),
+            None if grad_out is None else grad_out.data_ptr(), self.inverse.data_ptr(),
+            self.workspace.data_ptr(), self.workspace_bytes, self._stream,
+        )

@@ -218,6 +218,28 @@ int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows,
                           int64_t *unique_count, void *workspace,
                           size_t workspace_bytes, void *stream);
 
+/* The two halves of flare_pooled_backward, sharing one workspace:
+ * flare_pooled_dedup needs only the ids (it can run as soon as the batch is
+ * known, e.g. right after the forward), flare_pooled_apply consumes the
+ * pooled gradient and the dedup left in the workspace (same n, num_tables,
+ * batch, rows, dim and pooling).  unique_out / first_indices_out /
+ * unique_count are written by the dedup, inverse_out by the apply. */
+int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
+                       const int64_t *offsets, int32_t num_tables, int64_t batch,
+                       const int64_t *row_base, int64_t rows, int32_t dim,
+                       int32_t pooling, int64_t *unique_out,
+                       int64_t *first_indices_out, int64_t *unique_count,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                       float *state0, float *state1, int32_t *step,
+                       const flare_optimizer *optimizer, int64_t n,
+                       int32_t num_tables, int64_t batch, int32_t pooling,
+                       const float *weights, const float *pooled_grad,
+                       int32_t normalization_steps, float *grad_out,
+                       int32_t *inverse_out, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
 /* Reads back and clears the device-side error word that kernels set when they
  * meet an out-of-range index (written as 0 / ignored) or an exhausted
  * spin-wait guard.  Synchronizes the stream.  Returns the flag bits. */
