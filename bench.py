@@ -123,6 +123,8 @@ def main() -> int:
     ap.add_argument("--batches", type=int, default=8, help="pre-generated id batches to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--serial", action="store_true",
+                    help="run the dedup after the forward on one stream instead of overlapping them")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -182,7 +184,9 @@ def main() -> int:
     shard.synchronize()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    overlap = not args.serial
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    aux = torch.cuda.Stream(device=device)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     order = []
@@ -192,12 +196,24 @@ def main() -> int:
         order.append(k)
         ev = events[i]
         ev[0].record(stream)
-        p.forward()
-        ev[1].record(stream)
-        p.dedup()
-        ev[2].record(stream)
+        if overlap:
+            # dedup (ids only) on a second stream, concurrent with the forward
+            aux.wait_stream(stream)
+            ev[2].record(aux)
+            p._dedup_on(int(aux.cuda_stream))
+            ev[3].record(aux)
+            p.forward()
+            ev[1].record(stream)
+            stream.wait_event(ev[3])
+        else:
+            p.forward()
+            ev[1].record(stream)
+            ev[2].record(stream)
+            p.dedup()
+            ev[3].record(stream)
+        ev[4].record(stream)
         p.apply(grad, grad_out=grad_out, optimizer=none_opt)
-        ev[3].record(stream)
+        ev[5].record(stream)
     torch.cuda.synchronize()
     wall1 = time.perf_counter()
 
@@ -206,9 +222,9 @@ def main() -> int:
         k = order[i]
         b = batches[k]
         f = ev[0].elapsed_time(ev[1])
-        d = ev[1].elapsed_time(ev[2])
-        a = ev[2].elapsed_time(ev[3])
-        t = ev[0].elapsed_time(ev[3])
+        d = ev[2].elapsed_time(ev[3])
+        a = ev[4].elapsed_time(ev[5])
+        t = ev[0].elapsed_time(ev[5])
         step_ms.append(t)
         fwd_ms.append(f)
         dedup_ms.append(d)
@@ -253,6 +269,7 @@ def main() -> int:
             "forward_pooled_gather": statistics.median(fwd_ms),
             "dedup_sort_unique": statistics.median(dedup_ms),
             "segment_reduce_update": statistics.median(apply_ms),
+            "dedup_overlapped_with_forward": not args.serial,
         },
         "wall_ms_per_step": (wall1 - wall0) * 1e3 / args.steps,
         "roofline": {

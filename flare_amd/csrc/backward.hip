@@ -32,7 +32,7 @@ int bits_for(uint64_t max_value) {
 static size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool need_grad_row,
-                           bool need_aux, bool need_partials) {
+                           bool need_aux, bool need_partials, bool need_sums) {
   Workspace w{};
   w.n = n;
   w.key_bytes = key_bytes;
@@ -61,8 +61,8 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_rs = take((un + 1) * 4);
   const size_t o_rr = take(un * 4);
   const size_t o_ufr = take(static_cast<size_t>(w.units) * 4);
-  const size_t o_cross = take(static_cast<size_t>(w.units) * 4);
   const size_t o_part = need_partials ? take(static_cast<size_t>(w.units) * 2 * dim * 4) : 0;
+  const size_t o_sums = need_sums ? take(un * static_cast<size_t>(dim) * 4) : 0;
   w.total_bytes = off;
   if (base) {
     char *b = static_cast<char *>(base);
@@ -81,8 +81,8 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
     w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
     w.unit_first_run = reinterpret_cast<uint32_t *>(b + o_ufr);
-    w.cross_run = reinterpret_cast<uint32_t *>(b + o_cross);
     w.partial = need_partials ? reinterpret_cast<float *>(b + o_part) : nullptr;
+    w.sums = need_sums ? reinterpret_cast<float *>(b + o_sums) : nullptr;
   }
   return w;
 }
@@ -332,7 +332,14 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
       val[k] = 0;
     }
   }
+  // Stable rank inside the tile: for every item the lanes holding the same
+  // digit are found with wave64 ballots; the lowest of them adds the group's
+  // size to the wave's LDS counter of that digit (LDS atomics of one wave run
+  // in program order, so item k's groups precede item k+1's).  All atomics are
+  // issued before any result is consumed.
   const uint64_t lt = lanemask_lt();
+  uint32_t old[kSortItems];
+  uint32_t leader[kSortItems];
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
@@ -346,10 +353,13 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
       peers &= bit ? bb : ~bb;
     }
     const uint32_t before = __popcll(peers & lt);
-    const uint32_t c = valid ? s_wcnt[wave][d] : 0;
-    rank[k] = c + before;
-    if (valid && before == 0) s_wcnt[wave][d] = c + static_cast<uint32_t>(__popcll(peers));
+    leader[k] = valid ? static_cast<uint32_t>(__builtin_ctzll(peers)) : static_cast<uint32_t>(lane);
+    rank[k] = before;
+    old[k] = 0;
+    if (valid && before == 0) old[k] = atomicAdd(&s_wcnt[wave][d], static_cast<uint32_t>(__popcll(peers)));
   }
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) rank[k] += __shfl(old[k], static_cast<int>(leader[k]), 64);
   __syncthreads();
 
   // per digit: wave-exclusive prefixes, tile totals, tile-local and global bases
@@ -583,7 +593,7 @@ struct UpdateArgs {
   float norm;
   int dim;
   float *partial;
-  uint32_t *cross_run;
+  float *sums;  // [runs][dim] per-key gradient sums (optimizer modes)
   float *out;
   void *table;
   float *s0;
@@ -603,9 +613,40 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// Row state loaded ahead of the gradient sum (SGD / Adagrad rows, the
+// destination rank of a reduced gradient).
+template <int NC, int VEC>
+struct RowAhead {
+  float w[NC][VEC];
+  float s0;
+  int64_t dest;
+};
+
 template <typename Tag, int VEC, int G, int NC, int MODE>
-__device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, uint32_t key,
-                                             float (&g)[NC][VEC], int lane) {
+__device__ __forceinline__ void load_ahead(const UpdateArgs &a, uint32_t r, uint32_t key,
+                                           RowAhead<NC, VEC> &ahead, int lane) {
+  if constexpr (MODE == kModeUnique) {
+    ahead.dest = a.run_rank[r];
+  } else if constexpr (MODE == kModeSgd || MODE == kModeAdagrad) {
+    using E = typename Tag::elem;
+    const E *table = static_cast<const E *>(a.table);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (col < a.dim) {
+        load_as_f32<Tag, VEC>(table + static_cast<int64_t>(key) * a.dim + col, ahead.w[c]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) ahead.w[c][v] = 0.0f;
+      }
+    }
+    if constexpr (MODE == kModeAdagrad) ahead.s0 = a.s0[key];
+  }
+}
+
+template <typename Tag, int VEC, int G, int NC, int MODE>
+__device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, float (&g)[NC][VEC],
+                                             const RowAhead<NC, VEC> &ahead, int lane) {
   const int D = a.dim;
   if (a.use_norm) {
 #pragma unroll
@@ -614,8 +655,7 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, ui
       for (int v = 0; v < VEC; ++v) g[c][v] = g[c][v] / a.norm;
   }
   if constexpr (MODE == kModeRows || MODE == kModeUnique) {
-    const int64_t row = (MODE == kModeRows) ? static_cast<int64_t>(key)
-                                            : static_cast<int64_t>(a.run_rank[r]);
+    const int64_t row = (MODE == kModeRows) ? static_cast<int64_t>(key) : ahead.dest;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int col = (c * G + lane) * VEC;
@@ -635,16 +675,15 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, ui
           for (int v = 0; v < VEC; ++v) ss += static_cast<double>(g[c][v]) * static_cast<double>(g[c][v]);
       }
       ss = group_sum<G>(ss);
-      const float accn = static_cast<float>(static_cast<double>(a.s0[row]) + ss / static_cast<double>(D));
+      const float accn = static_cast<float>(static_cast<double>(ahead.s0) + ss / static_cast<double>(D));
       const float den = sqrtf(accn) + a.eps;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
         if (col >= D) continue;
         float w[VEC];
-        load_as_f32<Tag, VEC>(table + row * D + col, w);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) w[v] = w[v] - (a.lr * g[c][v]) / den;
+        for (int v = 0; v < VEC; ++v) w[v] = ahead.w[c][v] - (a.lr * g[c][v]) / den;
         store_from_f32<Tag, VEC>(table + row * D + col, w);
       }
       if (lane == 0) a.s0[row] = accn;
@@ -654,12 +693,11 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, ui
         const int col = (c * G + lane) * VEC;
         if (col >= D) continue;
         float w[VEC];
-        load_as_f32<Tag, VEC>(table + row * D + col, w);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) w[v] = w[v] - a.lr * g[c][v];
+        for (int v = 0; v < VEC; ++v) w[v] = ahead.w[c][v] - a.lr * g[c][v];
         store_from_f32<Tag, VEC>(table + row * D + col, w);
       }
-    } else {  // Adam
+    } else {  // Adam: m, v and the row are loaded here (too many registers to load ahead)
       const int32_t st = a.step[row] + 1;
       const float bc1 = static_cast<float>(1.0 - pow(a.b1d, static_cast<double>(st)));
       const float bc2 = static_cast<float>(1.0 - pow(a.b2d, static_cast<double>(st)));
@@ -689,12 +727,22 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t r, ui
   }
 }
 
+// Segment sums.  One group of G lanes per unit of kReduceUnit sorted
+// positions streams the unit's gradient rows four at a time, in order,
+// regardless of key boundaries; at each key head the running fp32 sum of the
+// finished piece is stored and restarted.  A piece holding a whole key goes
+// to its destination (the per-key sums for an optimizer, or straight to the
+// output for scatter / reduced gradients); a piece of a key that spans units
+// goes to this unit's partial slot (1 = the key's first piece, 0 = a later
+// one) for apply_kernel to fold.
 template <typename Tag, int VEC, int G, int NC, int MODE>
-__global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
+__global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   constexpr int kGroups = 256 / G;
   constexpr int kPPL = kReduceUnit / G;  // sorted positions per lane in the prefetch
+  constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
   __shared__ uint32_t s_grow[kGroups][kReduceUnit];
   __shared__ float s_scale[kGroups][kReduceUnit];
+  __shared__ uint32_t s_dest[kGroups][kReduceUnit + 1];
 
   const int lane = threadIdx.x % G;
   const int group = threadIdx.x / G;
@@ -706,11 +754,13 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
   const uint32_t j1 = active ? min(j0 + kReduceUnit, nvalid) : j0;
   const int cnt = static_cast<int>(j1 - j0);
   const int D = a.dim;
-  if (u < a.units && lane == 0) a.cross_run[u] = kNoRun;
+  const uint32_t r0 = active ? a.unit_first_run[u] : 0;
 
-  // Prefetch occurrence, gradient row and scale of every position of the unit.
+  // Prefetch occurrence, gradient row and scale of every position, the key
+  // heads, and (direct outputs) the destination row of each key in the unit.
   uint32_t occ[kPPL];
   uint64_t heads = 0;
+  const bool tail_head = !active || j1 >= nvalid || (a.sk[j1] != a.sk[j1 - 1]);
 #pragma unroll
   for (int q = 0; q < kPPL; ++q) {
     const int p = q * G + lane;
@@ -724,88 +774,105 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
         o = 0;
       }
       occ[q] = o;
-      head = (j == 0) || (a.sk[j] != a.sk[j - 1]);
+      const uint32_t key = a.sk[j];
+      head = (j == 0) || (key != a.sk[j - 1]);
       uint32_t gr = o;
       if (a.grad_mode == kGradRowDiv) gr = o / a.grad_div;
       else if (a.grad_mode == kGradRowArray) gr = a.grad_row[o];
       s_grow[group][p] = gr;
       s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f : a.scale[o];
+      if constexpr (MODE == kModeRows) s_dest[group][p] = key;
     }
     const uint64_t bal = __ballot(head);
     const uint64_t mine = (G == 64) ? bal : ((bal >> group_lane0) & ((1ull << G) - 1));
     heads |= mine << (q * G);
   }
+  if constexpr (MODE == kModeUnique) {
+    // keys of this unit: runs r0 .. r0 + (heads after position 0)
+    const int nruns = 1 + __popcll(heads & ~1ull);
+    for (int k = lane; k < nruns && active; k += G) s_dest[group][k] = a.run_rank[r0 + k];
+  }
   __syncthreads();
   if (!active) return;
 
-  uint32_t r = a.unit_first_run[u];
-  int p = 0;
-  while (p < cnt) {
-    // end of this piece: next head after p, or the end of the unit
-    const uint64_t later = (p + 1 < 64) ? (heads & (~0ull << (p + 1))) : 0ull;
-    const int e = later ? min(static_cast<int>(__builtin_ctzll(later)), cnt) : cnt;
-    float acc[NC][VEC];
+  uint32_t r = r0;
+  int piece_start = 0;
+  int piece_index = 0;
+  float acc[NC][VEC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
+
+  auto flush = [&](int end) {
+    const bool starts = piece_start > 0 || (heads & 1ull);
+    const bool whole = starts && (end < cnt || tail_head);
+    float *dst;
+    if (whole) {
+      if constexpr (MODE == kModeRows) {
+        dst = a.out + static_cast<int64_t>(s_dest[group][piece_start]) * D;
+      } else if constexpr (MODE == kModeUnique) {
+        dst = a.out + static_cast<int64_t>(s_dest[group][piece_index]) * D;
+      } else {
+        dst = a.sums + static_cast<int64_t>(r) * D;
+      }
+    } else {
+      dst = a.partial + (static_cast<size_t>(u) * 2 + (starts ? 1 : 0)) * D;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (kDirect && whole && a.use_norm) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[c][v] = acc[c][v] / a.norm;
+      }
+      if (col < D) store_f32<VEC>(dst + col, acc[c]);
 #pragma unroll
       for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
-    for (int pp = p; pp < e; pp += 4) {
-      float x[4][NC][VEC];
-      float sc[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bool ok = pp + t < e;
-        const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pp + t]) : 0;
-        sc[t] = ok ? s_scale[group][pp + t] : 0.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int col = (c * G + lane) * VEC;
-          if (ok && col < D) {
-            load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
-          } else {
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (pp + t >= e) break;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            float y = x[t][c][v];
-            if (a.scale_mode == kScaleMul) y = y * sc[t];
-            else if (a.scale_mode == kScaleDiv) y = y / sc[t];
-            acc[c][v] += y;
-          }
-      }
     }
+    ++r;
+    ++piece_index;
+    piece_start = end;
+  };
 
-    // finish the piece of run r
-    const uint32_t seg_start = a.run_start[r];
-    const uint32_t seg_end = a.run_start[r + 1];
-    if (seg_start >= j0 && seg_end <= j1) {
-      apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
-    } else {
-      // the key spans several units: keep this unit's partial for the fold
-      // (fixup_kernel, after this kernel); slot 1 = the key's first piece
-      const int slot = (seg_start < j0) ? 0 : 1;
-      float *mine = a.partial + (static_cast<size_t>(u) * 2 + slot) * D;
+  for (int pp = 0; pp < cnt; pp += 4) {
+    float x[4][NC][VEC];
+    float sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool ok = pp + t < cnt;
+      const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pp + t]) : 0;
+      sc[t] = ok ? s_scale[group][pp + t] : 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
-        if (col < D) store_f32<VEC>(mine + col, acc[c]);
+        if (ok && col < D) {
+          load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
+        }
       }
-      if (slot == 1 && lane == 0) a.cross_run[u] = r;
     }
-    ++r;
-    p = e;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int q = pp + t;
+      if (q >= cnt) break;
+      if (q > 0 && ((heads >> q) & 1ull)) flush(q);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          float y = x[t][c][v];
+          if (a.scale_mode == kScaleMul) y = y * sc[t];
+          else if (a.scale_mode == kScaleDiv) y = y / sc[t];
+          acc[c][v] += y;
+        }
+    }
   }
+  flush(cnt);
 
   if (a.inverse_out) {
-    const uint32_t r0 = a.unit_first_run[u];
 #pragma unroll
     for (int q = 0; q < kPPL; ++q) {
       const int pos = q * G + lane;
@@ -818,63 +885,72 @@ __global__ __launch_bounds__(256) void update_kernel(UpdateArgs a) {
   }
 }
 
-// Fold of keys whose occurrences span several units: the unit holding the
-// key's first piece (slot 1) sums it with the following units' continuation
-// partials (slot 0) left to right, then applies the update once.
+// Row-parallel apply over keys (runs), after sums_kernel.  A key whose
+// positions span several units is folded from the unit partials left to
+// right: the first unit's slot 1, then slot 0 of each following unit.  The
+// table row (and Adagrad accumulator) is loaded before the gradient.
 template <typename Tag, int VEC, int G, int NC, int MODE>
-__global__ __launch_bounds__(256) void fixup_kernel(UpdateArgs a) {
+__global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
   constexpr int kGroups = 256 / G;
+  constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
   const int lane = threadIdx.x % G;
-  const uint32_t u = blockIdx.x * kGroups + threadIdx.x / G;
-  if (u >= a.units) return;
-  const uint32_t r = a.cross_run[u];
-  if (r == kNoRun) return;
   const int D = a.dim;
-  const uint32_t seg_start = a.run_start[r];
-  const uint32_t seg_end = a.run_start[r + 1];
-  const uint32_t last = (seg_end - 1) / kReduceUnit;
-  float acc[NC][VEC];
-  const float *head = a.partial + (static_cast<size_t>(u) * 2 + 1) * D;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int col = (c * G + lane) * VEC;
-    if (col < D) {
-      load_f32<VEC>(head + col, acc[c]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
-    }
-  }
-  uint32_t x = u + 1;
-  for (; x + 4 <= last + 1; x += 4) {  // four partial loads in flight
-    float y[4][NC][VEC];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int col = (c * G + lane) * VEC;
-        if (col < D) load_f32<VEC>(a.partial + (static_cast<size_t>(x + t) * 2) * D + col, y[t][c]);
-      }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[c][v] += y[t][c][v];
-  }
-  for (; x <= last; ++x) {
+  const uint32_t runs = a.meta[1];
+  const uint32_t stride = gridDim.x * kGroups;
+  for (uint32_t r = blockIdx.x * kGroups + threadIdx.x / G; r < runs; r += stride) {
+    const uint32_t seg_start = a.run_start[r];
+    const uint32_t seg_end = a.run_start[r + 1];
+    if (seg_end <= seg_start || seg_end > a.n) continue;  // only after a tripped spin guard
+    const uint32_t h = seg_start / kReduceUnit;
+    const uint32_t last = (seg_end - 1) / kReduceUnit;
+    if (kDirect && h == last) continue;  // written by sums_kernel
+    const uint32_t key = a.sk[seg_start];
+    RowAhead<NC, VEC> ahead;
+    load_ahead<Tag, VEC, G, NC, MODE>(a, r, key, ahead, lane);
+    float g[NC][VEC];
+    const float *first = (h == last) ? a.sums + static_cast<int64_t>(r) * D
+                                     : a.partial + (static_cast<size_t>(h) * 2 + 1) * D;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int col = (c * G + lane) * VEC;
       if (col < D) {
-        float y[VEC];
-        load_f32<VEC>(a.partial + (static_cast<size_t>(x) * 2) * D + col, y);
+        load_f32<VEC>(first + col, g[c]);
+      } else {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[c][v] += y[v];
+        for (int v = 0; v < VEC; ++v) g[c][v] = 0.0f;
       }
     }
+    uint32_t x = h + 1;
+    for (; x + 4 <= last + 1; x += 4) {  // four partial loads in flight
+      float y[4][NC][VEC];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (col < D) load_f32<VEC>(a.partial + (static_cast<size_t>(x + t) * 2) * D + col, y[t][c]);
+        }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) g[c][v] += y[t][c][v];
+    }
+    for (; x <= last; ++x) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = (c * G + lane) * VEC;
+        if (col < D) {
+          float y[VEC];
+          load_f32<VEC>(a.partial + (static_cast<size_t>(x) * 2) * D + col, y);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) g[c][v] += y[v];
+        }
+      }
+    }
+    apply_update<Tag, VEC, G, NC, MODE>(a, key, g, ahead, lane);
   }
-  apply_update<Tag, VEC, G, NC, MODE>(a, r, a.sk[seg_start], acc, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -905,9 +981,13 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
+  // apply: grid-stride over the keys (their count is only known on the device)
+  auto apply_grid = [&](int g) {
+    return static_cast<int>(std::min<int64_t>(8192, std::max<int64_t>(1, ceil_div(a.n, 256 / g))));
+  };
 #define FLARE_UPDATE_PAIR(G_, NC_)                                             \
-  update_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);          \
-  fixup_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);
+  sums_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);            \
+  apply_kernel<Tag, VEC, G_, NC_, MODE><<<apply_grid(G_), 256, 0, s>>>(a);
   if (sh.nc == 1) {
     switch (sh.g) {
       case 8: FLARE_UPDATE_PAIR(8, 1) break;
@@ -1058,7 +1138,7 @@ int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipSt
   a.norm = static_cast<float>(norm_steps);
   a.dim = dim;
   a.partial = w.partial;
-  a.cross_run = w.cross_run;
+  a.sums = w.sums;
   a.out = out;
   a.table = table;
   a.s0 = s0;
@@ -1251,7 +1331,7 @@ extern "C" int flare_unique_first_occurrence(const void *values, int32_t key_dty
 // ----------------------------------------------------------------------------
 extern "C" size_t flare_sparse_update_workspace_bytes(int64_t n, int64_t rows, int32_t dim) {
   (void)rows;
-  return layout_workspace(nullptr, n, 4, std::max(dim, 1), false, false, true).total_bytes;
+  return layout_workspace(nullptr, n, 4, std::max(dim, 1), false, false, true, true).total_bytes;
 }
 
 extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
@@ -1270,7 +1350,7 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
   if (mode == kModeUnique) return fail(FLARE_ERR_ARGUMENT, "sparse update requires an optimizer (SGD, Adam or row-wise Adagrad)");
   FLARE_TRY(check_state(mode, state0, state1, step));
   if (n == 0 || rows == 0) return FLARE_OK;
-  Workspace w = layout_workspace(workspace, n, 4, dim, false, false, true);
+  Workspace w = layout_workspace(workspace, n, 4, dim, false, false, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
   int *err = device_error_word(&st);
@@ -1293,7 +1373,7 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
 // ----------------------------------------------------------------------------
 extern "C" size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows, int32_t dim) {
   (void)rows;
-  return layout_workspace(nullptr, n, 4, std::max(dim, 1), true, true, true).total_bytes;
+  return layout_workspace(nullptr, n, 4, std::max(dim, 1), true, true, true, true).total_bytes;
 }
 
 namespace flare {
@@ -1328,7 +1408,7 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
     if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
     return FLARE_OK;
   }
-  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true);
+  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
   int *err = device_error_word(&st);
@@ -1372,7 +1452,7 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
   FLARE_TRY(check_state(mode, state0, state1, step));
   if (n == 0 || batch * num_tables == 0) return FLARE_OK;
-  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true);
+  Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
   int *err = device_error_word(&st);
@@ -1396,7 +1476,7 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   a.norm = static_cast<float>(normalization_steps);
   a.dim = dim;
   a.partial = w.partial;
-  a.cross_run = w.cross_run;
+  a.sums = w.sums;
   a.out = grad_out;
   a.table = table;
   a.s0 = state0;

@@ -41,8 +41,8 @@ struct Workspace {
   uint32_t *run_start;    // [n + 1]
   uint32_t *run_rank;     // [n]
   uint32_t *unit_first_run;  // [units]
-  uint32_t *cross_run;    // [units] run whose head piece this unit holds, or kNoRun
   float *partial;         // [units][2][dim]
+  float *sums;            // [n][dim] per-key gradient sums (optimizer modes)
   size_t total_bytes;
   int64_t n;
   uint32_t tiles;
@@ -52,7 +52,7 @@ struct Workspace {
 
 // Computes the layout; with base == nullptr only sizes are filled in.
 Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool need_grad_row,
-                           bool need_aux, bool need_partials);
+                           bool need_aux, bool need_partials, bool need_sums = false);
 
 int bits_for(uint64_t max_value);
 

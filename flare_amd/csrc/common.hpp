@@ -206,23 +206,33 @@ __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_
     return 0;
   }
   publish(mine, kFlagAggregate | value);
+  // Walk back over predecessors, four status words per round trip.
   uint32_t prefix = 0;
   int64_t t = static_cast<int64_t>(tile) - 1;
   uint32_t spins = 0;
-  while (t >= 0) {
-    const uint32_t s = peek(status + static_cast<size_t>(t) * stride + idx);
-    const uint32_t flag = s & ~kCountMask;
-    if (flag == 0) {
-      if (++spins > kSpinLimit) {
-        record_error(err, kErrSpinGuard);
-        break;
+  bool done = false;
+  while (t >= 0 && !done) {
+    uint32_t seen[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      seen[w] = (t - w >= 0) ? peek(status + static_cast<size_t>(t - w) * stride + idx) : kFlagPrefix;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (done) break;
+      uint32_t st = seen[w];
+      while ((st & ~kCountMask) == 0) {  // predecessor has not published yet
+        if (++spins > kSpinLimit) {
+          record_error(err, kErrSpinGuard);
+          st = kFlagPrefix;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        st = peek(status + static_cast<size_t>(t - w) * stride + idx);
       }
-      __builtin_amdgcn_s_sleep(1);
-      continue;
+      prefix += st & kCountMask;
+      if ((st & ~kCountMask) == kFlagPrefix) done = true;
     }
-    prefix += s & kCountMask;
-    if (flag == kFlagPrefix) break;
-    --t;
+    t -= 4;
   }
   publish(mine, kFlagPrefix | ((prefix + value) & kCountMask));
   return prefix;

@@ -70,12 +70,32 @@ struct PooledArgs {
 
 constexpr int kBagsPerGroup = 4;
 
-template <typename Tag, int VEC, int G, bool kCsr, typename IdT>
+// Resolve one id to a table row (or -1 for a pad / out-of-range slot).
+template <bool kCsr, typename IdT>
+__device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, int64_t row_lo,
+                                               int64_t row_hi) {
+  const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
+  if constexpr (kCsr) {
+    if (id >= 0 && id < row_hi - row_lo) return row_lo + id;
+    record_error(a.err, kErrIndexOutOfRange);
+    return -1;
+  } else {
+    if (id == a.pad_index) return -1;
+    if (id >= 0 && id < a.table_rows) return id;
+    record_error(a.err, kErrIndexOutOfRange);
+    return -1;
+  }
+}
+
+// A group of G lanes pools one bag at a time; lane l holds L vectors of VEC
+// elements at columns (q*G + l)*VEC.  The first id chunk of each of the
+// group's four bags is loaded up front, so one-id bags cost one dependent row
+// load; longer bags load G ids at once (one per lane) and two rows ahead.
+template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   using E = typename Tag::elem;
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
-  constexpr int B4 = kBagsPerGroup;
   __shared__ int64_t s_off[kBagsPerBlock + 1];
 
   const int lane = threadIdx.x % G;
@@ -96,123 +116,114 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   const int D = a.dim;
   const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
 
-  // The group's bags (consecutive groups take consecutive bags).
-  int64_t begin[B4], len[B4], row_lo[B4], row_hi[B4], out_row[B4];
-  int64_t max_len = 0;
+  int64_t begin[kBagsPerGroup], end[kBagsPerGroup], lo[kBagsPerGroup], hi[kBagsPerGroup];
+  int64_t first_row[kBagsPerGroup];
+  float first_w[kBagsPerGroup];
 #pragma unroll
-  for (int j = 0; j < B4; ++j) {
+  for (int j = 0; j < kBagsPerGroup; ++j) {
     const int local = j * kGroups + group;
-    begin[j] = 0;
-    len[j] = 0;
-    row_lo[j] = 0;
-    row_hi[j] = a.table_rows;
-    out_row[j] = -1;
+    begin[j] = end[j] = 0;
+    lo[j] = 0;
+    hi[j] = a.table_rows;
+    first_row[j] = -1;
+    first_w[j] = 1.0f;
     if (local < nbags) {
       const int64_t bag = bag0 + local;
       if constexpr (kCsr) {
         begin[j] = s_off[local];
-        len[j] = s_off[local + 1] - begin[j];
-        if (len[j] < 0) len[j] = 0;
+        end[j] = s_off[local + 1];
         const int64_t t = bag / a.batch;
-        const int64_t b = bag - t * a.batch;
-        row_lo[j] = a.row_base[t];
-        row_hi[j] = a.row_base[t + 1];
-        out_row[j] = b * a.num_tables + t;
+        lo[j] = a.row_base[t];
+        hi[j] = a.row_base[t + 1];
       } else {
         begin[j] = bag * a.max_elements;
-        len[j] = a.max_elements;
-        out_row[j] = bag;
+        end[j] = begin[j] + a.max_elements;
       }
-      max_len = len[j] > max_len ? len[j] : max_len;
+      const int64_t i = begin[j] + lane;
+      if (i < end[j]) {
+        first_row[j] = resolve_row<kCsr, IdT>(a, i, lo[j], hi[j]);
+        if (weighted) first_w[j] = a.weights[i];
+      }
     }
   }
 
-  for (int c0 = 0; c0 < D; c0 += G * VEC) {
-    const int col = c0 + lane * VEC;
-    const bool col_ok = col < D;
-    float acc[B4][VEC];
-    int count[B4];
-#pragma unroll
-    for (int j = 0; j < B4; ++j) {
-      count[j] = 0;
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[j][v] = 0.0f;
+#pragma unroll 1
+  for (int j = 0; j < kBagsPerGroup; ++j) {
+    const int local = j * kGroups + group;
+    if (local >= nbags) break;
+    const int64_t bag = bag0 + local;
+    int64_t out_row = bag;
+    if constexpr (kCsr) {
+      const int64_t t = bag / a.batch;
+      out_row = (bag - t * a.batch) * a.num_tables + t;
     }
-    for (int64_t k0 = 0; k0 < max_len; k0 += G) {
-      // one id (and weight) per lane for each of the four bags
-      int64_t my_row[B4];
-      float my_w[B4];
+    for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
+      float acc[L][VEC];
 #pragma unroll
-      for (int j = 0; j < B4; ++j) {
-        my_row[j] = -1;
-        my_w[j] = 1.0f;
-        const int64_t e = k0 + lane;
-        if (e < len[j]) {
-          const int64_t i = begin[j] + e;
-          const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
-          if constexpr (kCsr) {
-            if (id >= 0 && id < row_hi[j] - row_lo[j]) {
-              my_row[j] = row_lo[j] + id;
-            } else {
-              record_error(a.err, kErrIndexOutOfRange);
-            }
-          } else if (id != a.pad_index) {
-            if (id >= 0 && id < a.table_rows) {
-              my_row[j] = id;
-            } else {
-              record_error(a.err, kErrIndexOutOfRange);
+      for (int q = 0; q < L; ++q)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
+      int count = 0;
+      for (int64_t base = begin[j]; base < end[j]; base += G) {
+        int64_t my_row = first_row[j];
+        float my_w = first_w[j];
+        if (base != begin[j]) {
+          my_row = -1;
+          my_w = 1.0f;
+          const int64_t i = base + lane;
+          if (i < end[j]) {
+            my_row = resolve_row<kCsr, IdT>(a, i, lo[j], hi[j]);
+            if (weighted) my_w = a.weights[i];
+          }
+        }
+        const int n = (end[j] - base) < G ? static_cast<int>(end[j] - base) : G;
+        for (int k = 0; k < n; k += 2) {
+          int64_t rows[2];
+          float w[2];
+          float x[2][L][VEC];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int src = (k + h < n) ? (k + h) : 0;
+            rows[h] = __shfl(my_row, src, G);
+            w[h] = __shfl(my_w, src, G);
+            if (k + h >= n) rows[h] = -1;
+#pragma unroll
+            for (int q = 0; q < L; ++q) {
+              const int col = c0 + (q * G + lane) * VEC;
+              if (rows[h] >= 0 && col < D) {
+                load_as_f32<Tag, VEC>(table + rows[h] * D + col, x[h][q]);
+              } else {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) x[h][q][v] = 0.0f;
+              }
             }
           }
-          if (weighted) my_w[j] = a.weights[i];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if (rows[h] < 0) continue;
+            ++count;
+#pragma unroll
+            for (int q = 0; q < L; ++q)
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) {
+                if (weighted) acc[q][v] += w[h] * x[h][q][v];
+                else acc[q][v] += x[h][q][v];
+              }
+          }
         }
       }
-      const int64_t remain = max_len - k0;
-      const int n = remain < G ? static_cast<int>(remain) : G;
-      for (int k = 0; k < n; k += 2) {
-        // two elements of each of the four bags: eight row loads in flight
-        int64_t rows[2][B4];
-        float w[2][B4];
-        float x[2][B4][VEC];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int j = 0; j < B4; ++j) {
-            const int src = (k + h < n) ? (k + h) : 0;
-            rows[h][j] = __shfl(my_row[j], src, G);
-            w[h][j] = __shfl(my_w[j], src, G);
-            if (k + h >= n) rows[h][j] = -1;
-            if (rows[h][j] >= 0 && col_ok) {
-              load_as_f32<Tag, VEC>(table + rows[h][j] * D + col, x[h][j]);
-            } else {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) x[h][j][v] = 0.0f;
-            }
-          }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int j = 0; j < B4; ++j) {
-            if (rows[h][j] < 0) continue;
-            ++count[j];
-            if (weighted) {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[j][v] += w[h][j] * x[h][j][v];
-            } else {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[j][v] += x[h][j][v];
-            }
-          }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < B4; ++j) {
-      if (out_row[j] < 0) continue;
       if (a.pooling == FLARE_POOL_MEAN) {
-        const float div = static_cast<float>(count[j] > 0 ? count[j] : 1);
+        const float div = static_cast<float>(count > 0 ? count : 1);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[j][v] = acc[j][v] / div;
+        for (int q = 0; q < L; ++q)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
       }
-      if (col_ok) store_from_f32<Tag, VEC>(out + out_row[j] * D + col, acc[j]);
+#pragma unroll
+      for (int q = 0; q < L; ++q) {
+        const int col = c0 + (q * G + lane) * VEC;
+        if (col < D) store_from_f32<Tag, VEC>(out + out_row * D + col, acc[q]);
+      }
     }
   }
 }
@@ -225,34 +236,37 @@ int grid_for(int64_t work, int64_t per_block) {
   return static_cast<int>(g < 1 ? 1 : (g > 0x7fffffff ? 0x7fffffff : g));
 }
 
-template <typename Tag, int VEC, bool kCsr, typename IdT>
+template <typename Tag, int VEC, int L, bool kCsr, typename IdT>
 int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
   const int64_t per_block = (kThreads / G) * kBagsPerGroup;
   const int grid = grid_for(a.bags, per_block);
   switch (G) {
-    case 8: pooled_kernel<Tag, VEC, 8, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    case 16: pooled_kernel<Tag, VEC, 16, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    case 32: pooled_kernel<Tag, VEC, 32, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    default: pooled_kernel<Tag, VEC, 64, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 4: pooled_kernel<Tag, VEC, 4, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 8: pooled_kernel<Tag, VEC, 8, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 16: pooled_kernel<Tag, VEC, 16, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 32: pooled_kernel<Tag, VEC, 32, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    default: pooled_kernel<Tag, VEC, 64, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
   }
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }
 
-int group_size(int cols) {
-  int g = 8;
-  while (g < cols && g < 64) g <<= 1;
+int group_size(int vectors, int min_g) {
+  int g = min_g;
+  while (g < vectors && g < 64) g <<= 1;
   return g;
 }
 
 template <typename Tag, bool kCsr, typename IdT>
 int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   constexpr int kWide = 16 / sizeof(typename Tag::elem);
-  const int esz = sizeof(typename Tag::elem);
   const bool wide = (a.dim % kWide == 0) && aligned(a.table, 16) && aligned(a.out, 16);
-  if (wide) return launch_pooled_g<Tag, kWide, kCsr, IdT>(a, group_size(a.dim / kWide), s);
-  (void)esz;
-  return launch_pooled_g<Tag, 1, kCsr, IdT>(a, group_size(a.dim), s);
+  if (wide) {
+    const int vectors = a.dim / kWide;  // 16-byte vectors per row
+    if (vectors >= 8) return launch_pooled_g<Tag, kWide, 2, kCsr, IdT>(a, group_size(vectors / 2, 4), s);
+    return launch_pooled_g<Tag, kWide, 1, kCsr, IdT>(a, group_size(vectors, 4), s);
+  }
+  return launch_pooled_g<Tag, 1, 1, kCsr, IdT>(a, group_size(a.dim, 8), s);
 }
 
 template <bool kCsr, typename IdT>

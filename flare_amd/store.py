@@ -494,6 +494,30 @@ class PooledStepPlan:
             self.workspace = torch.empty(max(self.workspace_bytes, 1), dtype=torch.uint8, device=dev)
         self._id_code = _native.INT32 if self.ids.dtype == torch.int32 else _native.INT64
         self._stream = int(shard.stream.cuda_stream)
+        self._dedup_stream: torch.cuda.Stream | None = None
+
+    def step(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
+             grad_out: torch.Tensor | None = None, optimizer: Any = None) -> torch.Tensor:
+        """Forward, dedup and apply of one training step, dedup overlapped with forward.
+
+        The dedup depends only on the ids, so it runs on a second stream (same
+        default priority) while the forward pools rows on the shard's stream;
+        the apply waits for both.  The dedup also waits for everything already
+        queued on the shard's stream, so it never overwrites a workspace an
+        earlier apply of this plan still reads.
+        """
+        main = self.shard.stream
+        if self._dedup_stream is None:
+            self._dedup_stream = torch.cuda.Stream(device=self.shard.device)
+        aux = self._dedup_stream
+        aux.wait_stream(main)
+        self._dedup_on(int(aux.cuda_stream))
+        done = torch.cuda.Event()
+        done.record(aux)
+        pooled = self.forward()
+        main.wait_event(done)
+        self.apply(pooled_grad, normalization_steps, grad_out, optimizer)
+        return pooled
 
     def forward(self) -> torch.Tensor:
         s = self.shard
@@ -507,12 +531,15 @@ class PooledStepPlan:
         return self.pooled
 
     def dedup(self) -> None:
+        self._dedup_on(self._stream)
+
+    def _dedup_on(self, stream: int) -> None:
         s = self.shard
         _native.call(
             "flare_pooled_dedup", self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
             s.num_tables, self.batch, s.row_base.data_ptr(), s.total_rows, s.dim,
             _POOLING[self.pooling], self.unique.data_ptr(), self.first_indices.data_ptr(),
-            self.unique_count.data_ptr(), self.workspace.data_ptr(), self.workspace_bytes, self._stream,
+            self.unique_count.data_ptr(), self.workspace.data_ptr(), self.workspace_bytes, stream,
         )
 
     def apply(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,

@@ -109,3 +109,32 @@ def test_reduced_gradients_bit_exact(gpu_device, no_device_errors, pooling):
                              storage=w.value_dtype, pooling=pooling, weights=w.weights)
     np.testing.assert_array_equal(_host(pooled), ep)
     no_device_errors()
+
+
+def test_overlapped_step_plan_matches_oracle(gpu_device, no_device_errors):
+    """PooledStepPlan.step: dedup on a second stream concurrent with the forward."""
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    w = make_workload(2, batch=3000, row_scale=0.0005)
+    shard = _shard(w, "rowwise_adagrad")
+    table0 = _host(shard.table.clone())
+    grad = torch.from_numpy(pooled_grad_host(w)).to(gpu_device)
+    plan = shard.plan_step(w.ids, w.offsets, w.batch)
+    state = {"acc": np.zeros(w.total_rows, np.float32)}
+    table = table0
+    for _ in range(2):  # the second step reads rows the first one updated
+        pooled = plan.step(grad)
+        shard.synchronize()
+        e_pooled, table, state, e_unique, e_inverse, e_first = O.pooled_step(
+            table, state, w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad.cpu().numpy(),
+            storage=w.value_dtype)
+        np.testing.assert_array_equal(_host(pooled), e_pooled)
+        u = int(plan.unique_count.item())
+        np.testing.assert_array_equal(plan.unique[:u].cpu().numpy(), e_unique)
+        np.testing.assert_array_equal(plan.first_indices[:u].cpu().numpy(), e_first)
+        np.testing.assert_array_equal(plan.inverse[:w.num_ids].cpu().numpy(), e_inverse)
+        ulps = O.storage_ulp_distance(_host(shard.table), table, w.value_dtype)
+        assert ulps.max() <= 1
+        table = _host(shard.table)  # continue from the device state (ulp-level ties)
+        state = {"acc": shard.state.state0.cpu().numpy()}
+    no_device_errors()
