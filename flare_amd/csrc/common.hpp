@@ -91,6 +91,25 @@ template <> struct Raw<8> { using type = uint2; };
 template <> struct Raw<4> { using type = uint32_t; };
 template <> struct Raw<2> { using type = uint16_t; };
 
+// Raw (still packed) vector of VEC storage elements and its conversion to f32;
+// kept packed while loads are in flight so that several rows fit in registers.
+template <typename Tag, int VEC>
+using RawVec = typename Raw<VEC * sizeof(typename Tag::elem)>::type;
+
+template <typename Tag, int VEC>
+__device__ __forceinline__ RawVec<Tag, VEC> load_raw(const typename Tag::elem *p) {
+  return *reinterpret_cast<const RawVec<Tag, VEC> *>(p);
+}
+
+template <typename Tag, int VEC>
+__device__ __forceinline__ void raw_to_f32(const RawVec<Tag, VEC> &raw, float (&out)[VEC]) {
+  using E = typename Tag::elem;
+  E tmp[VEC];
+  __builtin_memcpy(tmp, &raw, sizeof(raw));
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) out[i] = Tag::to_f32(tmp[i]);
+}
+
 // Load VEC consecutive storage elements (aligned to VEC*sizeof(elem)) as f32.
 template <typename Tag, int VEC>
 __device__ __forceinline__ void load_as_f32(const typename Tag::elem *p, float (&out)[VEC]) {

@@ -1,15 +1,14 @@
 // Forward kernels: row gather and pooled gather (padded [B,F,M] and CSR).
 //
-// Pooled gather layout on gfx950: a bag is owned by a group of G lanes of one
-// wave64; lane l of the group owns columns [l*VEC, l*VEC+VEC) (+ k*G*VEC),
-// loaded as one 16-byte vector per row (VEC = 8 for fp16/bf16, 4 for fp32),
-// so a D=128 bf16 row is one 256-byte transaction of 16 lanes and a wave
-// pools 4 bags at once.  The block's bag boundaries (CSR offsets) are staged
-// in LDS with one coalesced load; each group then reads its bag's ids G at a
-// time (one per lane, coalesced) and broadcasts them with ds_bpermute.
-// Accumulation is fp32, sequential in occurrence order (the reference's
-// order, gpu_cupy.py:96-103), and rows are loaded four at a time ahead of the
-// adds to keep several 16-byte loads in flight per lane.
+// Pooled gather layout on gfx950: a group of G lanes of one wave64 pools a
+// run of consecutive bags; lane l of the group owns columns
+// [l*VEC, l*VEC+VEC) (+ q*G*VEC), loaded as 16-byte vectors (VEC = 8 for
+// fp16/bf16, 4 for fp32), so a D=128 bf16 row is read by 8 lanes with two
+// 16-byte loads each and a wave pools 8 bags side by side.  The block's bag
+// boundaries (CSR offsets) are staged in LDS with one coalesced load; each
+// group reads its ids G at a time (one per lane, coalesced) and broadcasts
+// them with ds_bpermute.  Accumulation is fp32, sequential in occurrence
+// order (the reference's order, gpu_cupy.py:96-103).
 #include "common.hpp"
 
 namespace flare {
@@ -87,15 +86,20 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
   }
 }
 
-// A group of G lanes pools one bag at a time; lane l holds L vectors of VEC
-// elements at columns (q*G + l)*VEC.  The first id chunk of each of the
-// group's four bags is loaded up front, so one-id bags cost one dependent row
-// load; longer bags load G ids at once (one per lane) and two rows ahead.
+// A group of G lanes pools kBagsPerGroup consecutive bags; lane l holds L
+// vectors of VEC elements at columns (q*G + l)*VEC.  The group streams the
+// ids of its bags as one run (G ids per lane-parallel load), gathers rows
+// kDepth at a time regardless of bag boundaries (packed, so four rows of
+// loads are in flight per lane), accumulates in occurrence order, and stores
+// a bag's pooled row when the stream passes the bag's end.  One-id bags thus
+// cost a single round of dependent row loads per four bags.
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   using E = typename Tag::elem;
+  using R = RawVec<Tag, VEC>;
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
+  constexpr int kDepth = 4;
   __shared__ int64_t s_off[kBagsPerBlock + 1];
 
   const int lane = threadIdx.x % G;
@@ -103,128 +107,117 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * kBagsPerBlock;
   const int64_t nbags = (a.bags - bag0) < kBagsPerBlock ? (a.bags - bag0) : kBagsPerBlock;
 
-  if constexpr (kCsr) {
-    for (int i = threadIdx.x; i <= nbags; i += kThreads) {
+  for (int i = threadIdx.x; i <= nbags; i += kThreads) {
+    if constexpr (kCsr) {
       const int64_t o = a.offsets[bag0 + i];
       s_off[i] = o < 0 ? 0 : (o > a.num_ids ? a.num_ids : o);
+    } else {
+      s_off[i] = (bag0 + i) * a.max_elements;
     }
-    __syncthreads();
   }
+  __syncthreads();
+
+  const int lb0 = group * kBagsPerGroup;  // first bag of this group, block-local
+  const int nb = static_cast<int>(nbags - lb0 < kBagsPerGroup ? nbags - lb0 : kBagsPerGroup);
+  if (nb <= 0) return;
+  const int64_t s = s_off[lb0];
+  int64_t e = s_off[lb0 + nb];
+  if (e < s) e = s;  // decreasing offsets: pool nothing rather than read out of range
 
   const E *table = static_cast<const E *>(a.table);
   E *out = static_cast<E *>(a.out);
   const int D = a.dim;
   const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
+  const bool mean = a.pooling == FLARE_POOL_MEAN;
 
-  int64_t begin[kBagsPerGroup], end[kBagsPerGroup], lo[kBagsPerGroup], hi[kBagsPerGroup];
-  int64_t first_row[kBagsPerGroup];
-  float first_w[kBagsPerGroup];
+  for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
+    float acc[L][VEC];
 #pragma unroll
-  for (int j = 0; j < kBagsPerGroup; ++j) {
-    const int local = j * kGroups + group;
-    begin[j] = end[j] = 0;
-    lo[j] = 0;
-    hi[j] = a.table_rows;
-    first_row[j] = -1;
-    first_w[j] = 1.0f;
-    if (local < nbags) {
-      const int64_t bag = bag0 + local;
+    for (int q = 0; q < L; ++q)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
+    int count = 0;
+    int cur = 0;  // bag being pooled, group-local
+
+    auto flush = [&]() {
+      const int64_t bag = bag0 + lb0 + cur;
+      int64_t out_row = bag;
       if constexpr (kCsr) {
-        begin[j] = s_off[local];
-        end[j] = s_off[local + 1];
         const int64_t t = bag / a.batch;
-        lo[j] = a.row_base[t];
-        hi[j] = a.row_base[t + 1];
-      } else {
-        begin[j] = bag * a.max_elements;
-        end[j] = begin[j] + a.max_elements;
+        out_row = (bag - t * a.batch) * a.num_tables + t;
       }
-      const int64_t i = begin[j] + lane;
-      if (i < end[j]) {
-        first_row[j] = resolve_row<kCsr, IdT>(a, i, lo[j], hi[j]);
-        if (weighted) first_w[j] = a.weights[i];
-      }
-    }
-  }
-
-#pragma unroll 1
-  for (int j = 0; j < kBagsPerGroup; ++j) {
-    const int local = j * kGroups + group;
-    if (local >= nbags) break;
-    const int64_t bag = bag0 + local;
-    int64_t out_row = bag;
-    if constexpr (kCsr) {
-      const int64_t t = bag / a.batch;
-      out_row = (bag - t * a.batch) * a.num_tables + t;
-    }
-    for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
-      float acc[L][VEC];
-#pragma unroll
-      for (int q = 0; q < L; ++q)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
-      int count = 0;
-      for (int64_t base = begin[j]; base < end[j]; base += G) {
-        int64_t my_row = first_row[j];
-        float my_w = first_w[j];
-        if (base != begin[j]) {
-          my_row = -1;
-          my_w = 1.0f;
-          const int64_t i = base + lane;
-          if (i < end[j]) {
-            my_row = resolve_row<kCsr, IdT>(a, i, lo[j], hi[j]);
-            if (weighted) my_w = a.weights[i];
-          }
-        }
-        const int n = (end[j] - base) < G ? static_cast<int>(end[j] - base) : G;
-        for (int k = 0; k < n; k += 2) {
-          int64_t rows[2];
-          float w[2];
-          float x[2][L][VEC];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int src = (k + h < n) ? (k + h) : 0;
-            rows[h] = __shfl(my_row, src, G);
-            w[h] = __shfl(my_w, src, G);
-            if (k + h >= n) rows[h] = -1;
-#pragma unroll
-            for (int q = 0; q < L; ++q) {
-              const int col = c0 + (q * G + lane) * VEC;
-              if (rows[h] >= 0 && col < D) {
-                load_as_f32<Tag, VEC>(table + rows[h] * D + col, x[h][q]);
-              } else {
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) x[h][q][v] = 0.0f;
-              }
-            }
-          }
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            if (rows[h] < 0) continue;
-            ++count;
-#pragma unroll
-            for (int q = 0; q < L; ++q)
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) {
-                if (weighted) acc[q][v] += w[h] * x[h][q][v];
-                else acc[q][v] += x[h][q][v];
-              }
-          }
-        }
-      }
-      if (a.pooling == FLARE_POOL_MEAN) {
-        const float div = static_cast<float>(count > 0 ? count : 1);
-#pragma unroll
-        for (int q = 0; q < L; ++q)
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
-      }
+      const float div = static_cast<float>(count > 0 ? count : 1);
 #pragma unroll
       for (int q = 0; q < L; ++q) {
+        if (mean) {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
+        }
         const int col = c0 + (q * G + lane) * VEC;
         if (col < D) store_from_f32<Tag, VEC>(out + out_row * D + col, acc[q]);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
+      }
+      count = 0;
+      ++cur;
+    };
+
+    for (int64_t base = s; base < e; base += G) {
+      int64_t my_row = -1;
+      float my_w = 1.0f;
+      const int64_t i = base + lane;
+      if (i < e) {
+        int64_t lo = 0, hi = a.table_rows;
+        if constexpr (kCsr) {
+          int k = 0;  // bag of position i within the group
+#pragma unroll
+          for (int j = 1; j < kBagsPerGroup; ++j) k += (j < nb && i >= s_off[lb0 + j]) ? 1 : 0;
+          const int64_t t = (bag0 + lb0 + k) / a.batch;
+          lo = a.row_base[t];
+          hi = a.row_base[t + 1];
+        }
+        my_row = resolve_row<kCsr, IdT>(a, i, lo, hi);
+        if (weighted) my_w = a.weights[i];
+      }
+      const int n = (e - base) < G ? static_cast<int>(e - base) : G;
+      for (int k = 0; k < n; k += kDepth) {
+        R raw[kDepth][L];
+        int64_t rows[kDepth];
+        float w[kDepth];
+#pragma unroll
+        for (int h = 0; h < kDepth; ++h) {
+          const int src = (k + h < n) ? (k + h) : 0;
+          rows[h] = __shfl(my_row, src, G);
+          w[h] = weighted ? __shfl(my_w, src, G) : 1.0f;
+          if (k + h >= n) rows[h] = -1;
+#pragma unroll
+          for (int q = 0; q < L; ++q) {
+            const int col = c0 + (q * G + lane) * VEC;
+            if (rows[h] >= 0 && col < D) raw[h][q] = load_raw<Tag, VEC>(table + rows[h] * D + col);
+            else raw[h][q] = R{};
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < kDepth; ++h) {
+          if (k + h >= n) break;
+          const int64_t p = base + k + h;
+          while (cur < nb - 1 && p >= s_off[lb0 + cur + 1]) flush();
+          if (rows[h] < 0) continue;
+          ++count;
+#pragma unroll
+          for (int q = 0; q < L; ++q) {
+            float x[VEC];
+            raw_to_f32<Tag, VEC>(raw[h][q], x);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+              if (weighted) acc[q][v] += w[h] * x[v];
+              else acc[q][v] += x[v];
+            }
+          }
+        }
       }
     }
+    while (cur < nb) flush();  // the last bag and any empty bags after it
   }
 }
 

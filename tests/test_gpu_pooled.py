@@ -138,3 +138,49 @@ def test_overlapped_step_plan_matches_oracle(gpu_device, no_device_errors):
         table = _host(shard.table)  # continue from the device state (ulp-level ties)
         state = {"acc": shard.state.state0.cpu().numpy()}
     no_device_errors()
+
+
+RAGGED = [
+    # batch, dim, max bag length (bags of length 0 included)
+    (1, 128, 9),     # each group of four bags spans four tables
+    (3, 24, 70),     # bags longer than one id chunk; 3-vector rows
+    (7, 20, 5),      # dim not a multiple of the 16-byte vector: scalar lanes
+    (130, 300, 3),   # fp32 rows of 300 (two vectors per lane)
+    (5, 1100, 4),    # several column passes
+]
+
+
+@pytest.mark.parametrize("storage", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("pooling", ["sum", "mean", "weighted"])
+@pytest.mark.parametrize("case", range(len(RAGGED)))
+def test_csr_ragged_bags_bit_exact(gpu_device, no_device_errors, storage, pooling, case):
+    """Empty bags, bags spanning id chunks and tables, every row shape: forward and reduced grads."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    batch, dim, max_len = RAGGED[case]
+    rng = np.random.default_rng(100 + case)
+    table_rows = [5, 40, 17]
+    lengths = rng.integers(0, max_len + 1, size=len(table_rows) * batch)
+    lengths[::4] = 0
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    ids = (rng.integers(0, 1 << 30, size=int(offsets[-1])) % np.asarray(table_rows)[bag_table]).astype(np.int64)
+    weights = rng.uniform(0, 1, size=ids.size).astype(np.float32)
+    shard = PooledTableShard(table_rows, dim, value_dtype=storage, initializer=Uniform(-1.0, 1.0), seed=case)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    w = weights if pooling == "weighted" else None
+    pooled = shard.lookup_pooled(ids, offsets, batch, pooling=pooling, per_sample_weights=w)
+    grad = rng.normal(0, 1, size=(batch, len(table_rows), dim)).astype(np.float32)
+    unique, inverse, first, g = shard.reduce_pooled_gradients(ids, offsets, batch, grad, pooling=pooling,
+                                                              per_sample_weights=w)
+    shard.synchronize()
+    expected = O.gather_pooled_csr(_host(shard.table), ids, offsets, row_base, batch, dim, storage=storage,
+                                   pooling=pooling, weights=w)
+    np.testing.assert_array_equal(_host(pooled), expected)
+    eu, ei, ef, eg = O.pooled_grad_sums(ids, offsets, row_base, batch, dim, grad, pooling=pooling, weights=w)
+    np.testing.assert_array_equal(unique.cpu().numpy(), eu)
+    np.testing.assert_array_equal(inverse.cpu().numpy(), ei)
+    np.testing.assert_array_equal(first.cpu().numpy(), ef)
+    np.testing.assert_array_equal(g.cpu().numpy(), eg)
+    no_device_errors()
