@@ -37,6 +37,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   w.n = n;
   w.key_bytes = key_bytes;
   w.tiles = static_cast<uint32_t>(ceil_div(std::max<int64_t>(n, 1), kSortTile));
+  w.sort_tiles = static_cast<uint32_t>(ceil_div(std::max<int64_t>(n, 1), kOneTile));
   w.units = static_cast<uint32_t>(ceil_div(std::max<int64_t>(n, 1), kReduceUnit));
   const size_t un = static_cast<size_t>(std::max<int64_t>(n, 1));
   size_t off = 0;
@@ -48,7 +49,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_hist = take(static_cast<size_t>(kHistCopies) * kMaxPasses * kRadix * 4);
   const size_t o_tickets = take(16 * 4);
   const size_t o_meta = take(4 * 4);
-  const size_t o_sort_status = take(static_cast<size_t>(8) * w.tiles * kRadix * 4);
+  const size_t o_sort_status = take(static_cast<size_t>(8) * w.sort_tiles * kRadix * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
   w.zero_bytes = off;
   const size_t o_k0 = take(un * key_bytes);
@@ -296,34 +297,36 @@ __global__ void init_minmax_kernel(unsigned long long *out) {
 // onesweep radix pass (stable)
 // ----------------------------------------------------------------------------
 template <typename K>
-__global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
+__global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     const K *__restrict__ kin, const uint32_t *__restrict__ vin, K *__restrict__ kout,
     uint32_t *__restrict__ vout, uint32_t n, int pass, const uint32_t *__restrict__ hist,
     uint32_t *status, uint32_t *ticket, int *err) {
+  constexpr int kWaves = kOneThreads / 64;
+  static_assert(kOneThreads >= kRadix, "one thread per digit");
   const int shift = pass * kRadixBits;
   __shared__ uint32_t s_tile;
-  __shared__ uint32_t s_wcnt[4][kRadix];
+  __shared__ uint32_t s_wcnt[kWaves][kRadix];
   __shared__ uint32_t s_tile_start[kRadix];
   __shared__ uint32_t s_gbase[kRadix];
-  __shared__ uint32_t s_scan[8];
-  __shared__ K s_keys[kSortTile];
-  __shared__ uint32_t s_vals[kSortTile];
+  __shared__ uint32_t s_scan[2][kWaves];
+  __shared__ K s_keys[kOneTile];
+  __shared__ uint32_t s_vals[kOneTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   if (tid == 0) s_tile = atomicAdd(ticket, 1u);
-  for (int i = tid; i < 4 * kRadix; i += kSortThreads) (&s_wcnt[0][0])[i] = 0;
+  for (int i = tid; i < kWaves * kRadix; i += kOneThreads) (&s_wcnt[0][0])[i] = 0;
   __syncthreads();
   const uint32_t tile = s_tile;
-  const uint32_t base = tile * kSortTile;
+  const uint32_t base = tile * kOneTile;
 
-  K key[kSortItems];
-  uint32_t val[kSortItems];
-  uint32_t rank[kSortItems];
+  K key[kOneItems];
+  uint32_t val[kOneItems];
+  uint32_t rank[kOneItems];
 #pragma unroll
-  for (int k = 0; k < kSortItems; ++k) {
-    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+  for (int k = 0; k < kOneItems; ++k) {
+    const uint32_t e = base + wave * (kOneItems * 64) + k * 64 + lane;
     if (e < n) {
       key[k] = kin[e];
       val[k] = vin ? vin[e] : e;
@@ -333,16 +336,14 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     }
   }
   // Stable rank inside the tile: for every item the lanes holding the same
-  // digit are found with wave64 ballots; the lowest of them adds the group's
-  // size to the wave's LDS counter of that digit (LDS atomics of one wave run
-  // in program order, so item k's groups precede item k+1's).  All atomics are
-  // issued before any result is consumed.
+  // digit are found with wave64 ballots; the lowest of them advances the
+  // wave's LDS counter of that digit by the group's size.  The counter reads
+  // and writes of one wave stay in program order, so item k's groups precede
+  // item k+1's.
   const uint64_t lt = lanemask_lt();
-  uint32_t old[kSortItems];
-  uint32_t leader[kSortItems];
 #pragma unroll
-  for (int k = 0; k < kSortItems; ++k) {
-    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+  for (int k = 0; k < kOneItems; ++k) {
+    const uint32_t e = base + wave * (kOneItems * 64) + k * 64 + lane;
     const bool valid = e < n;
     const uint32_t d = valid ? (static_cast<uint32_t>(key[k] >> shift) & (kRadix - 1)) : 0;
     uint64_t peers = __ballot(valid);
@@ -353,33 +354,37 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
       peers &= bit ? bb : ~bb;
     }
     const uint32_t before = __popcll(peers & lt);
-    leader[k] = valid ? static_cast<uint32_t>(__builtin_ctzll(peers)) : static_cast<uint32_t>(lane);
-    rank[k] = before;
-    old[k] = 0;
-    if (valid && before == 0) old[k] = atomicAdd(&s_wcnt[wave][d], static_cast<uint32_t>(__popcll(peers)));
+    const uint32_t c = valid ? s_wcnt[wave][d] : 0;
+    rank[k] = c + before;
+    if (valid && before == 0) s_wcnt[wave][d] = c + static_cast<uint32_t>(__popcll(peers));
   }
-#pragma unroll
-  for (int k = 0; k < kSortItems; ++k) rank[k] += __shfl(old[k], static_cast<int>(leader[k]), 64);
   __syncthreads();
 
-  // per digit: wave-exclusive prefixes, tile totals, tile-local and global bases
-  const int d = tid;  // kRadix == kSortThreads
-  const uint32_t c0 = s_wcnt[0][d], c1 = s_wcnt[1][d], c2 = s_wcnt[2][d], c3 = s_wcnt[3][d];
-  const uint32_t total = c0 + c1 + c2 + c3;
-  s_wcnt[0][d] = 0;
-  s_wcnt[1][d] = c0;
-  s_wcnt[2][d] = c0 + c1;
-  s_wcnt[3][d] = c0 + c1 + c2;
-  const uint32_t tile_start = block_exclusive_scan_256(total, s_scan, nullptr);
-  const uint32_t digit_base = block_exclusive_scan_256(digit_total(hist, pass, d), s_scan + 4, nullptr);
-  const uint32_t prefix = lookback_exclusive(status, tile, kRadix, d, total, err);
-  s_tile_start[d] = tile_start;
-  s_gbase[d] = digit_base + prefix;
+  // per digit (thread d < kRadix): wave-exclusive prefixes, tile totals,
+  // tile-local and global bases
+  const int d = tid;
+  uint32_t total = 0;
+  if (d < kRadix) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const uint32_t c = s_wcnt[w][d];
+      s_wcnt[w][d] = total;
+      total += c;
+    }
+  }
+  const uint32_t tile_start = block_exclusive_scan<kOneThreads>(total, s_scan[0]);
+  const uint32_t digit_base =
+      block_exclusive_scan<kOneThreads>(d < kRadix ? digit_total(hist, pass, d) : 0u, s_scan[1]);
+  if (d < kRadix) {
+    const uint32_t prefix = lookback_exclusive(status, tile, kRadix, d, total, err);
+    s_tile_start[d] = tile_start;
+    s_gbase[d] = digit_base + prefix;
+  }
   __syncthreads();
 
 #pragma unroll
-  for (int k = 0; k < kSortItems; ++k) {
-    const uint32_t e = base + wave * (kSortItems * 64) + k * 64 + lane;
+  for (int k = 0; k < kOneItems; ++k) {
+    const uint32_t e = base + wave * (kOneItems * 64) + k * 64 + lane;
     if (e < n) {
       const uint32_t dk = static_cast<uint32_t>(key[k] >> shift) & (kRadix - 1);
       const uint32_t pos = s_tile_start[dk] + s_wcnt[wave][dk] + rank[k];
@@ -388,8 +393,8 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     }
   }
   __syncthreads();
-  const uint32_t count = (n - base) < static_cast<uint32_t>(kSortTile) ? (n - base) : kSortTile;
-  for (uint32_t p = tid; p < count; p += kSortThreads) {
+  const uint32_t count = (n - base) < static_cast<uint32_t>(kOneTile) ? (n - base) : kOneTile;
+  for (uint32_t p = tid; p < count; p += kOneThreads) {
     const K kk = s_keys[p];
     const uint32_t dk = static_cast<uint32_t>(kk >> shift) & (kRadix - 1);
     const uint32_t out = s_gbase[dk] + (p - s_tile_start[dk]);
@@ -1042,10 +1047,10 @@ int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result)
   const uint32_t n = static_cast<uint32_t>(w.n);
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
-    onesweep_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
+    onesweep_kernel<K><<<w.sort_tiles, kOneThreads, 0, s>>>(
         static_cast<const K *>(w.keys[cur]), p == 0 ? nullptr : w.vals[cur],
         static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p,
-        w.hist, w.sort_status + static_cast<size_t>(p) * w.tiles * kRadix,
+        w.hist, w.sort_status + static_cast<size_t>(p) * w.sort_tiles * kRadix,
         w.tickets + p, err);
     FLARE_TRY_HIP(hipGetLastError());
     cur ^= 1;

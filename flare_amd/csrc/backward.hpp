@@ -8,6 +8,10 @@ namespace flare {
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 occurrences per tile
+// Radix passes use larger tiles: 1024 threads x 8 keys (one tile per CU).
+constexpr int kOneThreads = 1024;
+constexpr int kOneItems = 8;
+constexpr int kOneTile = kOneThreads * kOneItems;
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 // Sorted positions are reduced in units of kReduceUnit consecutive positions;
@@ -29,7 +33,7 @@ struct Workspace {
   uint32_t *hist;         // [kHistCopies][kMaxPasses][kRadix] digit histograms
   uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
   uint32_t *meta;         // [4]: nvalid, unique count
-  uint32_t *sort_status;  // [8][tiles][kRadix]
+  uint32_t *sort_status;  // [8][sort_tiles][kRadix]
   uint32_t *scan_status;  // [2][tiles]
   size_t zero_bytes;
   // not initialized
@@ -45,7 +49,8 @@ struct Workspace {
   float *sums;            // [n][dim] per-key gradient sums (optimizer modes)
   size_t total_bytes;
   int64_t n;
-  uint32_t tiles;
+  uint32_t tiles;       // kSortTile tiles (scans)
+  uint32_t sort_tiles;  // kOneTile tiles (radix passes)
   uint32_t units;
   int key_bytes;
 };

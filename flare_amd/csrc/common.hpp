@@ -188,6 +188,29 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
   return wave_base + incl - v;
 }
 
+// Exclusive scan of one uint32 per thread over a block of THREADS threads.
+// scratch: >= THREADS/64 uint32 of LDS.  Every thread of the block must call it.
+template <int THREADS>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *scratch) {
+  constexpr int kWaves = THREADS / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  uint32_t wave_base = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+    if (w < wave) wave_base += scratch[w];
+  __syncthreads();
+  return wave_base + incl - v;
+}
+
 // ----------------------------------------------------------------------------
 // Decoupled look-back (single-pass chained scan across tiles).
 //
