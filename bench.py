@@ -123,6 +123,9 @@ def main() -> int:
     ap.add_argument("--batches", type=int, default=8, help="pre-generated id batches to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="before timing, run a plain device-to-device copy of this many MiB three times "
+                         "(a kernel of known traffic, to scale FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--serial", action="store_true",
                     help="run the dedup after the forward on one stream instead of overlapping them")
     args = ap.parse_args()
@@ -172,6 +175,15 @@ def main() -> int:
     for p in plans:
         uniques.append(int(p.unique_count.item()))
     log(f"setup {time.time() - t_setup:.1f}s: N={[p.n for p in plans][:3]}..., U={uniques[:3]}...")
+
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x {args.copy_mib} MiB read + {args.copy_mib} MiB written")
+        del src, dst
 
     def run(p):
         p.forward()

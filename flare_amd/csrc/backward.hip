@@ -51,17 +51,24 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_meta = take(4 * 4);
   const size_t o_sort_status = take(static_cast<size_t>(8) * w.sort_tiles * kRadix * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
+  const size_t o_head_bits = take(static_cast<size_t>(ceil_div(std::max<int64_t>(n, 1), 32)) * 4);
   w.zero_bytes = off;
   const size_t o_k0 = take(un * key_bytes);
   const size_t o_k1 = take(un * key_bytes);
   const size_t o_v0 = take(un * 4);
   const size_t o_v1 = take(un * 4);
   const size_t o_grow = need_grad_row ? take(un * 4) : 0;
+  const size_t o_sgr = need_grad_row ? take(un * 4) : 0;
+  const size_t o_rgr = need_grad_row ? take(un * 4) : 0;
   const size_t o_aux = need_aux ? take(un * 4) : 0;
-  const size_t o_roo = take(un * 4);
+  const size_t o_ssc = need_aux ? take(un * 4) : 0;
+  const size_t o_rsc = need_aux ? take(un * 4) : 0;
+  const size_t o_head_run = take(un * 4);
   const size_t o_rs = take((un + 1) * 4);
   const size_t o_rr = take(un * 4);
+  const size_t o_rk = take(un * 4);
   const size_t o_ufr = take(static_cast<size_t>(w.units) * 4);
+  const size_t o_hot = take(static_cast<size_t>(w.units) * 4);
   const size_t o_part = need_partials ? take(static_cast<size_t>(w.units) * 2 * dim * 4) : 0;
   const size_t o_sums = need_sums ? take(un * static_cast<size_t>(dim) * 4) : 0;
   w.total_bytes = off;
@@ -78,10 +85,17 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.vals[1] = reinterpret_cast<uint32_t *>(b + o_v1);
     w.grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_grow) : nullptr;
     w.aux = need_aux ? reinterpret_cast<float *>(b + o_aux) : nullptr;
-    w.run_of_occ = reinterpret_cast<uint32_t *>(b + o_roo);
+    w.sorted_grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_sgr) : nullptr;
+    w.sorted_scale = need_aux ? reinterpret_cast<float *>(b + o_ssc) : nullptr;
+    w.run_grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_rgr) : nullptr;
+    w.run_scale = need_aux ? reinterpret_cast<float *>(b + o_rsc) : nullptr;
+    w.head_bits = reinterpret_cast<uint32_t *>(b + o_head_bits);
+    w.head_run = reinterpret_cast<uint32_t *>(b + o_head_run);
     w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
     w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
+    w.run_key = reinterpret_cast<uint32_t *>(b + o_rk);
     w.unit_first_run = reinterpret_cast<uint32_t *>(b + o_ufr);
+    w.hot_runs = reinterpret_cast<uint32_t *>(b + o_hot);
     w.partial = need_partials ? reinterpret_cast<float *>(b + o_part) : nullptr;
     w.sums = need_sums ? reinterpret_cast<float *>(b + o_sums) : nullptr;
   }
@@ -145,7 +159,6 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
                                                           int64_t key_limit, int has_pad,
                                                           int64_t pad, int passes,
                                                           uint32_t *__restrict__ keys,
-                                                          uint32_t *__restrict__ run_of_occ,
                                                           uint32_t *__restrict__ hist, int *err) {
   __shared__ uint32_t s_hist[4 * kRadix];
   for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
@@ -162,7 +175,6 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
       }
     }
     keys[i] = k;
-    if (k == sentinel) run_of_occ[i] = kInvalidRun;
     add_histograms(s_hist, k, passes);
   }
   __syncthreads();
@@ -185,8 +197,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
-    float *__restrict__ aux, uint32_t *__restrict__ run_of_occ, uint32_t *__restrict__ hist,
-    int *err) {
+    float *__restrict__ aux, uint32_t *__restrict__ hist, int *err) {
   __shared__ uint32_t s_hist[4 * kRadix];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
@@ -221,7 +232,6 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
       k = static_cast<uint32_t>(lo_row + id);
     } else {
       record_error(err, kErrIndexOutOfRange);
-      run_of_occ[i] = kInvalidRun;
     }
     keys[i] = k;
     grad_row[i] = static_cast<uint32_t>(b * num_tables + t);
@@ -447,19 +457,90 @@ __device__ __forceinline__ void tile_flag_scan(const bool (&flag)[kSortItems], u
 // ----------------------------------------------------------------------------
 // runs: segment heads of the sorted keys
 // ----------------------------------------------------------------------------
+// Number of key heads (first position of each distinct valid key) in each
+// kSortTile tile of the sorted keys; the counts are then scanned by
+// scan_counts_kernel so that every tile of runs_kernel knows its first run.
+template <typename K>
+__global__ __launch_bounds__(kSortThreads) void head_count_kernel(const K *__restrict__ sk,
+                                                                 uint32_t n, K sentinel,
+                                                                 int use_sentinel,
+                                                                 uint32_t *__restrict__ counts) {
+  __shared__ uint32_t s_sum[kSortThreads / 64];
+  const uint32_t base = blockIdx.x * kSortTile;
+  uint32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const uint32_t j = base + k * kSortThreads + threadIdx.x;
+    if (j < n) {
+      const K key = sk[j];
+      const bool valid = !(use_sentinel && key == sentinel);
+      c += (valid && (j == 0 || sk[j - 1] != key)) ? 1u : 0u;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
+  if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / 64; ++w) t += s_sum[w];
+    counts[blockIdx.x] = t;
+  }
+}
+
+// First occurrences (bits of head_bits) in each kSortTile tile of occurrences.
+__global__ __launch_bounds__(kSortThreads) void first_count_kernel(const uint32_t *__restrict__ head_bits,
+                                                                  uint32_t n,
+                                                                  uint32_t *__restrict__ counts) {
+  static_assert(kSortTile / 32 <= kSortThreads, "one bitmap word per thread");
+  const uint32_t word = blockIdx.x * (kSortTile / 32) + threadIdx.x;
+  uint32_t c = 0;
+  if (threadIdx.x < kSortTile / 32 && word < (n + 31) / 32) c = __popc(head_bits[word]);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
+  __shared__ uint32_t s_sum[kSortThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / 64; ++w) t += s_sum[w];
+    counts[blockIdx.x] = t;
+  }
+}
+
+// In-place exclusive scan of per-tile counts: one block of 1024 threads.
+__global__ __launch_bounds__(1024) void scan_counts_kernel(uint32_t *counts, uint32_t tiles) {
+  __shared__ uint32_t s_scan[16];
+  __shared__ uint32_t s_carry;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (uint32_t b = 0; b < tiles; b += 1024) {
+    const uint32_t i = b + threadIdx.x;
+    const uint32_t v = i < tiles ? counts[i] : 0u;
+    const uint32_t ex = block_exclusive_scan<1024>(v, s_scan);
+    const uint32_t carry = s_carry;
+    if (i < tiles) counts[i] = carry + ex;
+    __syncthreads();
+    if (threadIdx.x == 1023) s_carry = carry + ex + v;
+    __syncthreads();
+  }
+}
+
 template <typename K>
 __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     const K *__restrict__ sk, const uint32_t *__restrict__ sv, uint32_t n, K sentinel,
     int use_sentinel, uint32_t *__restrict__ run_start, uint32_t *__restrict__ unit_first_run,
-    uint32_t *__restrict__ run_of_occ, uint32_t *__restrict__ meta, uint32_t *status,
-    uint32_t *ticket, int *err) {
-  __shared__ uint32_t s_tile;
+    uint32_t *__restrict__ head_bits, uint32_t *__restrict__ head_run,
+    uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix,
+    uint32_t *__restrict__ run_key,
+    const uint32_t *__restrict__ grad_row, const float *__restrict__ scale,
+    uint32_t *__restrict__ sorted_grad_row, float *__restrict__ sorted_scale,
+    uint32_t *__restrict__ run_grad_row, float *__restrict__ run_scale) {
   __shared__ uint32_t s_cnt[160];
-  __shared__ uint32_t s_prefix;
   const int tid = threadIdx.x;
-  if (tid == 0) s_tile = atomicAdd(ticket, 1u);
-  __syncthreads();
-  const uint32_t tile = s_tile;
+  const uint32_t tile = blockIdx.x;
   const uint32_t base = tile * kSortTile;
   bool valid[kSortItems], head[kSortItems];
   K key[kSortItems];
@@ -477,9 +558,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
   FlagScan fs;
   uint32_t total;
   tile_flag_scan(head, s_cnt, fs, &total);
-  if (tid == 0) s_prefix = lookback_exclusive(status, tile, 1, 0, total, err);
-  __syncthreads();
-  const uint32_t prefix = s_prefix;
+  const uint32_t prefix = head_prefix[tile];  // heads before this tile
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     const uint32_t j = base + k * kSortThreads + tid;
@@ -492,11 +571,31 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
       continue;
     }
     const uint32_t r = prefix + fs.incl[k] - 1;
-    if (r >= n) continue;  // only after a tripped spin guard
-    if (head[k]) run_start[r] = j;
+    if (r >= n) continue;
+    if (head[k]) {
+      run_start[r] = j;
+      if (run_key) run_key[r] = static_cast<uint32_t>(key[k]);
+    }
     if ((j % kReduceUnit) == 0) unit_first_run[j / kReduceUnit] = r;
     const uint32_t o = sv[j];
-    if (o < n) run_of_occ[o] = r | (head[k] ? kHeadBit : 0u);
+    if (o < n) {
+      if (head[k]) {
+        // first occurrence of the key (the sort is stable): mark it for rank_kernel
+        atomicOr(head_bits + (o >> 5), 1u << (o & 31));
+        head_run[o] = r;
+      }
+      // per sorted position: the gradient row and scale of its occurrence
+      if (sorted_grad_row) {
+        const uint32_t gr = grad_row[o];
+        sorted_grad_row[j] = gr;
+        if (head[k]) run_grad_row[r] = gr;
+      }
+      if (sorted_scale) {
+        const float sc = scale[o];
+        sorted_scale[j] = sc;
+        if (head[k]) run_scale[r] = sc;
+      }
+    }
     const bool last = (j + 1 == n) || (use_sentinel && sk[j + 1] == sentinel);
     if (last) {
       meta[0] = j + 1;
@@ -512,44 +611,33 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
 enum UniqueSource : int { kUniqueNone = 0, kUniqueFromValues = 1, kUniqueFromSorted = 2 };
 
 __global__ __launch_bounds__(kSortThreads) void rank_kernel(
-    const uint32_t *__restrict__ run_of_occ, uint32_t n, uint32_t *status, uint32_t *ticket,
-    uint32_t tiles, int *err, uint32_t *__restrict__ run_rank, int64_t *__restrict__ first_indices,
-    void *__restrict__ unique_out, int unique_source, const void *__restrict__ values,
-    int value_bytes, const uint32_t *__restrict__ sorted_keys,
-    const uint32_t *__restrict__ run_start, int64_t *__restrict__ unique_count) {
-  __shared__ uint32_t s_tile;
+    const uint32_t *__restrict__ head_bits, const uint32_t *__restrict__ head_run, uint32_t n,
+    const uint32_t *__restrict__ first_prefix, uint32_t tiles, uint32_t *__restrict__ run_rank,
+    int64_t *__restrict__ first_indices, void *__restrict__ unique_out, int unique_source,
+    const void *__restrict__ values, int value_bytes, const uint32_t *__restrict__ run_key,
+    int64_t *__restrict__ unique_count) {
   __shared__ uint32_t s_cnt[160];
-  __shared__ uint32_t s_prefix;
   const int tid = threadIdx.x;
-  if (tid == 0) s_tile = atomicAdd(ticket, 1u);
-  __syncthreads();
-  const uint32_t tile = s_tile;
+  const uint32_t tile = blockIdx.x;
   const uint32_t base = tile * kSortTile;
   bool first[kSortItems];
-  uint32_t ro[kSortItems];
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     const uint32_t i = base + k * kSortThreads + tid;
-    ro[k] = (i < n) ? run_of_occ[i] : kInvalidRun;
-    first[k] = (ro[k] & kHeadBit) != 0;
+    first[k] = (i < n) && ((head_bits[i >> 5] >> (i & 31)) & 1u);
   }
   FlagScan fs;
   uint32_t total;
   tile_flag_scan(first, s_cnt, fs, &total);
-  if (tid == 0) {
-    const uint32_t p = lookback_exclusive(status, tile, 1, 0, total, err);
-    s_prefix = p;
-    if (tile == tiles - 1 && unique_count) *unique_count = static_cast<int64_t>(p + total);
-  }
-  __syncthreads();
-  const uint32_t prefix = s_prefix;
+  const uint32_t prefix = first_prefix[tile];  // first occurrences before this tile
+  if (tid == 0 && tile == tiles - 1 && unique_count) *unique_count = static_cast<int64_t>(prefix + total);
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     if (!first[k]) continue;
     const uint32_t i = base + k * kSortThreads + tid;
     const uint32_t rank = prefix + fs.incl[k] - 1;
-    const uint32_t r = ro[k] & ~kHeadBit;
-    if (rank >= n || r >= n) continue;  // only after a tripped spin guard
+    const uint32_t r = head_run[i];
+    if (rank >= n || r >= n) continue;
     run_rank[r] = rank;
     if (first_indices) first_indices[rank] = i;
     if (unique_source == kUniqueFromValues) {
@@ -558,19 +646,29 @@ __global__ __launch_bounds__(kSortThreads) void rank_kernel(
       else
         static_cast<uint32_t *>(unique_out)[rank] = static_cast<const uint32_t *>(values)[i];
     } else if (unique_source == kUniqueFromSorted) {
-      const uint32_t at = run_start[r];
-      if (at < n) static_cast<int64_t *>(unique_out)[rank] = static_cast<int64_t>(sorted_keys[at]);
+      static_cast<int64_t *>(unique_out)[rank] = static_cast<int64_t>(run_key[r]);
     }
   }
 }
 
-__global__ __launch_bounds__(256) void inverse_kernel(const uint32_t *__restrict__ run_of_occ,
+// inverse[occurrence] = rank of its key, one wave64 per unit of sorted positions.
+template <typename K>
+__global__ __launch_bounds__(256) void inverse_kernel(const K *__restrict__ sk,
+                                                     const uint32_t *__restrict__ sv, uint32_t n,
+                                                     const uint32_t *__restrict__ unit_first_run,
                                                      const uint32_t *__restrict__ run_rank,
-                                                     int64_t n, int32_t *__restrict__ inverse) {
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
-    const uint32_t ro = run_of_occ[i];
-    inverse[i] = (ro == kInvalidRun) ? -1 : static_cast<int32_t>(run_rank[ro & ~kHeadBit]);
-  }
+                                                     int32_t *__restrict__ inverse) {
+  static_assert(kReduceUnit == 64, "one wave per unit");
+  const uint32_t j = blockIdx.x * 256u + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool valid = j < n;
+  const bool head = valid && j > 0 && sk[j] != sk[j - 1];
+  const uint64_t heads = __ballot(head);
+  if (!valid) return;
+  const uint64_t le = (lane == 63) ? ~0ull : ((2ull << lane) - 1);
+  const uint32_t r = unit_first_run[j / kReduceUnit] + __popcll(heads & le & ~1ull);
+  const uint32_t o = sv[j];
+  if (o < n && r < n) inverse[o] = static_cast<int32_t>(run_rank[r]);
 }
 
 // ----------------------------------------------------------------------------
@@ -594,11 +692,17 @@ struct UpdateArgs {
   const uint32_t *grad_row;
   int scale_mode;
   const float *scale;  // weights (kScaleMul) or divisors (kScaleDiv), per occurrence
+  const uint32_t *sorted_grad_row;  // gradient row per sorted position, or null
+  const float *sorted_scale;        // scale per sorted position, or null
+  const uint32_t *run_grad_row;     // gradient row of each key's first position (with sorted_grad_row)
+  const float *run_scale;           // scale of each key's first position (with sorted_scale)
   int use_norm;
   float norm;
   int dim;
   float *partial;
   float *sums;  // [runs][dim] per-key gradient sums (optimizer modes)
+  const uint32_t *run_key;
+  uint32_t *hot_runs;  // keys spanning more than kInlineSpan + 1 units (meta[2] of them)
   float *out;
   void *table;
   float *s0;
@@ -732,14 +836,37 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, 
   }
 }
 
-// Segment sums.  One group of G lanes per unit of kReduceUnit sorted
-// positions streams the unit's gradient rows four at a time, in order,
-// regardless of key boundaries; at each key head the running fp32 sum of the
-// finished piece is stored and restarted.  A piece holding a whole key goes
-// to its destination (the per-key sums for an optimizer, or straight to the
-// output for scatter / reduced gradients); a piece of a key that spans units
-// goes to this unit's partial slot (1 = the key's first piece, 0 = a later
-// one) for apply_kernel to fold.
+// A key is "short" when all its sorted positions lie in one unit and there
+// are at most kShortRun of them: apply_kernel sums its gradient rows itself
+// (all loads in flight at once), so no per-key sum is written for it.  Every
+// other key goes through sums_kernel.
+constexpr uint32_t kShortRun = 8;
+// A key whose positions span more than kInlineSpan + 1 units is "hot": its
+// unit partials are folded by a whole block (fold_kernel) instead of one
+// lane group of apply_kernel.
+constexpr uint32_t kInlineSpan = 8;
+
+__device__ __forceinline__ uint32_t grad_row_of(const UpdateArgs &a, uint32_t o) {
+  if (a.grad_mode == kGradRowDiv) return o / a.grad_div;
+  if (a.grad_mode == kGradRowArray) return a.grad_row[o];
+  return o;
+}
+
+__device__ __forceinline__ float scaled(const UpdateArgs &a, float x, float sc) {
+  if (a.scale_mode == kScaleMul) return x * sc;
+  if (a.scale_mode == kScaleDiv) return x / sc;
+  return x;
+}
+
+// Segment sums of the long keys.  One group of G lanes per unit of
+// kReduceUnit sorted positions lists the unit's positions that belong to long
+// keys and streams their gradient rows four at a time, in order; at each key
+// head the running fp32 sum of the finished piece is stored and restarted.  A
+// piece holding a whole key goes to its destination (the per-key sums for an
+// optimizer, or straight to the output for scatter / reduced gradients); a
+// piece of a key that spans units goes to this unit's partial slot (1 = the
+// key's first piece, 0 = a later one) for apply_kernel to fold.  The group
+// also writes the inverse (rank of the key) of every position of the unit.
 template <typename Tag, int VEC, int G, int NC, int MODE>
 __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   constexpr int kGroups = 256 / G;
@@ -747,11 +874,13 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
   __shared__ uint32_t s_grow[kGroups][kReduceUnit];
   __shared__ float s_scale[kGroups][kReduceUnit];
-  __shared__ uint32_t s_dest[kGroups][kReduceUnit + 1];
+  __shared__ uint32_t s_dest[kGroups][kReduceUnit];
+  __shared__ uint8_t s_list[kGroups][kReduceUnit];
 
   const int lane = threadIdx.x % G;
   const int group = threadIdx.x / G;
   const int group_lane0 = (threadIdx.x & 63) - lane;  // first lane of this group in the wave
+  const uint64_t group_mask = (G == 64) ? ~0ull : ((1ull << G) - 1);
   const uint32_t u = blockIdx.x * kGroups + group;
   const uint32_t nvalid = a.meta[0];
   const uint32_t j0 = u * kReduceUnit;
@@ -761,9 +890,9 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   const int D = a.dim;
   const uint32_t r0 = active ? a.unit_first_run[u] : 0;
 
-  // Prefetch occurrence, gradient row and scale of every position, the key
-  // heads, and (direct outputs) the destination row of each key in the unit.
+  // occurrence and key head of every position
   uint32_t occ[kPPL];
+  uint32_t keyv[kPPL];
   uint64_t heads = 0;
   const bool tail_head = !active || j1 >= nvalid || (a.sk[j1] != a.sk[j1 - 1]);
 #pragma unroll
@@ -771,6 +900,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
     const int p = q * G + lane;
     bool head = false;
     occ[q] = 0;
+    keyv[q] = 0;
     if (p < cnt) {
       const uint32_t j = j0 + p;
       uint32_t o = a.sv[j];
@@ -779,50 +909,84 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
         o = 0;
       }
       occ[q] = o;
-      const uint32_t key = a.sk[j];
-      head = (j == 0) || (key != a.sk[j - 1]);
-      uint32_t gr = o;
-      if (a.grad_mode == kGradRowDiv) gr = o / a.grad_div;
-      else if (a.grad_mode == kGradRowArray) gr = a.grad_row[o];
-      s_grow[group][p] = gr;
-      s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f : a.scale[o];
-      if constexpr (MODE == kModeRows) s_dest[group][p] = key;
+      keyv[q] = a.sk[j];
+      head = (j == 0) || (keyv[q] != a.sk[j - 1]);
     }
     const uint64_t bal = __ballot(head);
-    const uint64_t mine = (G == 64) ? bal : ((bal >> group_lane0) & ((1ull << G) - 1));
-    heads |= mine << (q * G);
+    heads |= ((bal >> group_lane0) & group_mask) << (q * G);
+  }
+  // long positions: their gradient row, scale and (scatter) destination key
+  uint64_t longmask = 0;
+#pragma unroll
+  for (int q = 0; q < kPPL; ++q) {
+    const int p = q * G + lane;
+    bool lng = false;
+    if (p < cnt) {
+      const uint64_t le = (p == 63) ? ~0ull : ((2ull << p) - 1);
+      const uint64_t below = heads & le;
+      const uint64_t above = heads & ~le;
+      const int ps = below ? 63 - __builtin_clzll(below) : -1;
+      const int pe = above ? __builtin_ctzll(above) : cnt;
+      const bool cross_right = (pe == cnt) && !tail_head;
+      lng = ps < 0 || cross_right || static_cast<uint32_t>(pe - ps) > kShortRun;
+      if (lng) {
+        const uint32_t j = j0 + p;
+        s_grow[group][p] = a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, occ[q]);
+        s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f
+                            : (a.sorted_scale ? a.sorted_scale[j] : a.scale[occ[q]]);
+        if constexpr (MODE == kModeRows) s_dest[group][p] = keyv[q];
+      }
+    }
+    const uint64_t bal = __ballot(lng);
+    longmask |= ((bal >> group_lane0) & group_mask) << (q * G);
+  }
+#pragma unroll
+  for (int q = 0; q < kPPL; ++q) {
+    const int p = q * G + lane;
+    if (p < cnt && ((longmask >> p) & 1ull))
+      s_list[group][__popcll(longmask & ((1ull << p) - 1))] = static_cast<uint8_t>(p);
   }
   if constexpr (MODE == kModeUnique) {
-    // keys of this unit: runs r0 .. r0 + (heads after position 0)
+    // rank of each key of the unit: runs r0 .. r0 + (heads after position 0)
     const int nruns = 1 + __popcll(heads & ~1ull);
-    for (int k = lane; k < nruns && active; k += G) s_dest[group][k] = a.run_rank[r0 + k];
+    for (int k = lane; k < nruns && active && longmask; k += G) s_dest[group][k] = a.run_rank[r0 + k];
   }
   __syncthreads();
   if (!active) return;
 
-  uint32_t r = r0;
-  int piece_start = 0;
-  int piece_index = 0;
+  const int nlong = __popcll(longmask);
   float acc[NC][VEC];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
+  int piece_first = -1;
+  int prev = 0;
 
-  auto flush = [&](int end) {
-    const bool starts = piece_start > 0 || (heads & 1ull);
-    const bool whole = starts && (end < cnt || tail_head);
+  auto flush = [&](int pf, int pl) {
+    const bool starts = (heads >> pf) & 1ull;
+    const bool ends_here = (pl + 1 < cnt) || tail_head;
+    const bool whole = starts && ends_here;
+    const uint64_t le = (pf == 63) ? ~0ull : ((2ull << pf) - 1);
+    const int k = __popcll(heads & ~1ull & le);  // key index within the unit
     float *dst;
     if (whole) {
       if constexpr (MODE == kModeRows) {
-        dst = a.out + static_cast<int64_t>(s_dest[group][piece_start]) * D;
+        dst = a.out + static_cast<int64_t>(s_dest[group][pf]) * D;
       } else if constexpr (MODE == kModeUnique) {
-        dst = a.out + static_cast<int64_t>(s_dest[group][piece_index]) * D;
+        dst = a.out + static_cast<int64_t>(s_dest[group][k]) * D;
       } else {
-        dst = a.sums + static_cast<int64_t>(r) * D;
+        dst = a.sums + static_cast<int64_t>(r0 + k) * D;
       }
     } else {
       dst = a.partial + (static_cast<size_t>(u) * 2 + (starts ? 1 : 0)) * D;
+      if (starts && lane == 0) {
+        // head piece of a key that continues past this unit: hot when the key
+        // still holds the position kInlineSpan + 1 units further on
+        const uint32_t probe = (u + kInlineSpan + 1) * kReduceUnit;
+        if (probe < nvalid && a.sk[probe] == a.sk[j0 + pf])
+          a.hot_runs[atomicAdd(const_cast<uint32_t *>(a.meta) + 2, 1u)] = r0 + k;
+      }
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -835,19 +999,18 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
     }
-    ++r;
-    ++piece_index;
-    piece_start = end;
   };
 
-  for (int pp = 0; pp < cnt; pp += 4) {
+  for (int i0 = 0; i0 < nlong; i0 += 4) {
     float x[4][NC][VEC];
     float sc[4];
+    int pos[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const bool ok = pp + t < cnt;
-      const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pp + t]) : 0;
-      sc[t] = ok ? s_scale[group][pp + t] : 0.0f;
+      const bool ok = i0 + t < nlong;
+      pos[t] = ok ? s_list[group][i0 + t] : 0;
+      const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pos[t]]) : 0;
+      sc[t] = ok ? s_scale[group][pos[t]] : 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
@@ -861,21 +1024,21 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int q = pp + t;
-      if (q >= cnt) break;
-      if (q > 0 && ((heads >> q) & 1ull)) flush(q);
+      if (i0 + t >= nlong) break;
+      const int p = pos[t];
+      if (piece_first >= 0 && ((heads >> p) & 1ull)) {
+        flush(piece_first, prev);
+        piece_first = -1;
+      }
+      if (piece_first < 0) piece_first = p;
+      prev = p;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          float y = x[t][c][v];
-          if (a.scale_mode == kScaleMul) y = y * sc[t];
-          else if (a.scale_mode == kScaleDiv) y = y / sc[t];
-          acc[c][v] += y;
-        }
+        for (int v = 0; v < VEC; ++v) acc[c][v] += scaled(a, x[t][c][v], sc[t]);
     }
   }
-  flush(cnt);
+  if (piece_first >= 0) flush(piece_first, prev);
 
   if (a.inverse_out) {
 #pragma unroll
@@ -890,71 +1053,200 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   }
 }
 
-// Row-parallel apply over keys (runs), after sums_kernel.  A key whose
-// positions span several units is folded from the unit partials left to
-// right: the first unit's slot 1, then slot 0 of each following unit.  The
-// table row (and Adagrad accumulator) is loaded before the gradient.
+// Row-parallel apply over keys (runs), after sums_kernel.  A short key's
+// gradient rows are summed here in occurrence order; a long key whose
+// positions lie in one unit takes its sum from sums_kernel; a key spanning
+// several units is folded from the unit partials left to right: the first
+// unit's slot 1, then slot 0 of each following unit.  The table row (and
+// Adagrad accumulator) is loaded before the gradient.
 template <typename Tag, int VEC, int G, int NC, int MODE>
 __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
   constexpr int kGroups = 256 / G;
   constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
+  static_assert(G >= static_cast<int>(kShortRun), "one lane per position of a short key");
   const int lane = threadIdx.x % G;
   const int D = a.dim;
   const uint32_t runs = a.meta[1];
   const uint32_t stride = gridDim.x * kGroups;
+  // fold_kernel (launched before) has read the hot-key count: clear it for
+  // the next update that reuses this dedup
+  if (blockIdx.x == 0 && threadIdx.x == 0) const_cast<uint32_t *>(a.meta)[2] = 0;
   for (uint32_t r = blockIdx.x * kGroups + threadIdx.x / G; r < runs; r += stride) {
     const uint32_t seg_start = a.run_start[r];
     const uint32_t seg_end = a.run_start[r + 1];
+    const uint32_t key = a.run_key[r];
     if (seg_end <= seg_start || seg_end > a.n) continue;  // only after a tripped spin guard
     const uint32_t h = seg_start / kReduceUnit;
     const uint32_t last = (seg_end - 1) / kReduceUnit;
-    if (kDirect && h == last) continue;  // written by sums_kernel
-    const uint32_t key = a.sk[seg_start];
+    const uint32_t len = seg_end - seg_start;
+    const bool is_short = (h == last) && len <= kShortRun;
+    if (kDirect && h == last && !is_short) continue;  // written by sums_kernel
+    if (last - h > kInlineSpan) continue;             // hot key: fold_kernel
     RowAhead<NC, VEC> ahead;
     load_ahead<Tag, VEC, G, NC, MODE>(a, r, key, ahead, lane);
     float g[NC][VEC];
-    const float *first = (h == last) ? a.sums + static_cast<int64_t>(r) * D
-                                     : a.partial + (static_cast<size_t>(h) * 2 + 1) * D;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int col = (c * G + lane) * VEC;
-      if (col < D) {
-        load_f32<VEC>(first + col, g[c]);
-      } else {
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) g[c][v] = 0.0f;
+      for (int v = 0; v < VEC; ++v) g[c][v] = 0.0f;
+    if (is_short) {
+      uint32_t my_gr = 0;
+      float my_sc = 1.0f;
+      if (len == 1 && a.sorted_grad_row && (a.scale_mode == kScaleNone || a.sorted_scale)) {
+        // one occurrence: its gradient row was recorded with the key
+        my_gr = a.run_grad_row[r];
+        if (a.scale_mode != kScaleNone) my_sc = a.run_scale[r];
+      } else if (static_cast<uint32_t>(lane) < len) {
+        const uint32_t j = seg_start + lane;
+        const bool need_occ = !a.sorted_grad_row || (a.scale_mode != kScaleNone && !a.sorted_scale);
+        uint32_t o = 0;
+        if (need_occ) {
+          o = a.sv[j];
+          if (o >= a.n) {
+            record_error(a.err, kErrSpinGuard);
+            o = 0;
+          }
+        }
+        my_gr = a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o);
+        if (a.scale_mode != kScaleNone) my_sc = a.sorted_scale ? a.sorted_scale[j] : a.scale[o];
       }
-    }
-    uint32_t x = h + 1;
-    for (; x + 4 <= last + 1; x += 4) {  // four partial loads in flight
-      float y[4][NC][VEC];
+      for (uint32_t k = 0; k < len; k += 4) {
+        float x[4][NC][VEC];
+        float sc[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
+          const bool ok = k + t < len;
+          const int src = ok ? static_cast<int>(k + t) : 0;
+          const int64_t gr = static_cast<int64_t>(__shfl(my_gr, src, G));
+          sc[t] = __shfl(my_sc, src, G);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int col = (c * G + lane) * VEC;
-          if (col < D) load_f32<VEC>(a.partial + (static_cast<size_t>(x + t) * 2) * D + col, y[t][c]);
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (ok && col < D) {
+              load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
+            } else {
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
+            }
+          }
         }
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
+          if (k + t >= len) break;
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
+          for (int c = 0; c < NC; ++c)
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) g[c][v] += y[t][c][v];
-    }
-    for (; x <= last; ++x) {
+            for (int v = 0; v < VEC; ++v) g[c][v] += scaled(a, x[t][c][v], sc[t]);
+        }
+      }
+    } else {
+      const float *first = (h == last) ? a.sums + static_cast<int64_t>(r) * D
+                                       : a.partial + (static_cast<size_t>(h) * 2 + 1) * D;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
-        if (col < D) {
-          float y[VEC];
-          load_f32<VEC>(a.partial + (static_cast<size_t>(x) * 2) * D + col, y);
+        if (col < D) load_f32<VEC>(first + col, g[c]);
+      }
+      uint32_t x = h + 1;
+      for (; x + 4 <= last + 1; x += 4) {  // four partial loads in flight
+        float y[4][NC][VEC];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) g[c][v] += y[v];
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (col < D) load_f32<VEC>(a.partial + (static_cast<size_t>(x + t) * 2) * D + col, y[t][c]);
+          }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) g[c][v] += y[t][c][v];
+      }
+      for (; x <= last; ++x) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (col < D) {
+            float y[VEC];
+            load_f32<VEC>(a.partial + (static_cast<size_t>(x) * 2) * D + col, y);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) g[c][v] += y[v];
+          }
         }
       }
     }
     apply_update<Tag, VEC, G, NC, MODE>(a, key, g, ahead, lane);
+  }
+}
+
+// Hot keys: one block per key folds the key's unit partials in order.  Each
+// round the block's lane groups load kFoldDepth partial rows each into LDS
+// (all loads in flight together), then group 0 adds them left to right: the
+// first unit's slot 1, then slot 0 of every following unit.  Group 0 then
+// applies the update.
+template <typename Tag, int VEC, int G, int NC, int MODE>
+__global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
+  constexpr int kGroups = 256 / G;
+  extern __shared__ float s_rows[];  // [kGroups * depth][dim]
+  const int lane = threadIdx.x % G;
+  const int group = threadIdx.x / G;
+  const int D = a.dim;
+  const uint32_t chunk = static_cast<uint32_t>(kGroups * depth);
+  const uint32_t hot = a.meta[2];
+  for (uint32_t i = blockIdx.x; i < hot; i += gridDim.x) {
+    const uint32_t r = a.hot_runs[i];
+    const uint32_t seg_start = a.run_start[r];
+    const uint32_t seg_end = a.run_start[r + 1];
+    const uint32_t key = a.run_key[r];
+    if (seg_end <= seg_start || seg_end > a.n) continue;  // block-uniform
+    const uint32_t h = seg_start / kReduceUnit;
+    const uint32_t last = (seg_end - 1) / kReduceUnit;
+    const uint32_t count = last - h + 1;  // partial rows to fold, in order
+    RowAhead<NC, VEC> ahead;
+    float g[NC][VEC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) g[c][v] = 0.0f;
+    if (group == 0) load_ahead<Tag, VEC, G, NC, MODE>(a, r, key, ahead, lane);
+    for (uint32_t base = 0; base < count; base += chunk) {
+      for (int t = 0; t < depth; ++t) {
+        const uint32_t k = base + group * depth + t;
+        if (k >= count) break;
+        const uint32_t x = h + k;
+        const float *src = a.partial + (static_cast<size_t>(x) * 2 + (k == 0 ? 1 : 0)) * D;
+        float *dst = s_rows + static_cast<size_t>(group * depth + t) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (col < D) {
+            float y[VEC];
+            load_f32<VEC>(src + col, y);
+            store_f32<VEC>(dst + col, y);
+          }
+        }
+      }
+      __syncthreads();
+      if (group == 0) {
+        const uint32_t m = min(chunk, count - base);
+        for (uint32_t k = 0; k < m; ++k) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (col < D) {
+              float y[VEC];
+              load_f32<VEC>(s_rows + static_cast<size_t>(k) * D + col, y);
+#pragma unroll
+              for (int v = 0; v < VEC; ++v) g[c][v] += y[v];
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (group == 0) apply_update<Tag, VEC, G, NC, MODE>(a, key, g, ahead, lane);
   }
 }
 
@@ -983,16 +1275,33 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
   return FLARE_OK;
 }
 
+// apply_kernel runs half-width lane groups (twice the columns per lane) where
+// the row allows, so that twice as many keys are in flight per wave.
+constexpr int kApplyG(int g, int nc) { return (g > 8 && nc == 1) ? g / 2 : g; }
+constexpr int kApplyNC(int g, int nc) { return (g > 8 && nc == 1) ? 2 : nc; }
+
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
-  // apply: grid-stride over the keys (their count is only known on the device)
+  // apply: one key per group where possible: the key count is only known on the
+  // device, so the grid covers n keys (capped) and idle groups exit at once
   auto apply_grid = [&](int g) {
-    return static_cast<int>(std::min<int64_t>(8192, std::max<int64_t>(1, ceil_div(a.n, 256 / g))));
+    return static_cast<int>(std::min<int64_t>(65536, std::max<int64_t>(1, ceil_div(a.n, 256 / g))));
   };
+  // fold: partial rows staged per round, at most 32 KiB of LDS
+  auto fold_depth = [&](int g) {
+    const int groups = 256 / g;
+    int depth = 4;
+    while (depth > 1 && static_cast<int64_t>(groups) * depth * a.dim * 4 > 32768) depth >>= 1;
+    return depth;
+  };
+  auto fold_lds = [&](int g) { return static_cast<size_t>(256 / g) * fold_depth(g) * a.dim * 4; };
+  const int fold_grid = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(a.units, kInlineSpan + 1))));
 #define FLARE_UPDATE_PAIR(G_, NC_)                                             \
   sums_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);            \
-  apply_kernel<Tag, VEC, G_, NC_, MODE><<<apply_grid(G_), 256, 0, s>>>(a);
+  fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
+  apply_kernel<Tag, VEC, kApplyG(G_, NC_), kApplyNC(G_, NC_), MODE>                 \
+      <<<apply_grid(kApplyG(G_, NC_)), 256, 0, s>>>(a);
   if (sh.nc == 1) {
     switch (sh.g) {
       case 8: FLARE_UPDATE_PAIR(8, 1) break;
@@ -1059,26 +1368,58 @@ int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result)
   return FLARE_OK;
 }
 
+// Runs and first-occurrence ranks of sorted keys: head counts per tile and
+// their scan, runs (run ids; each key's first occurrence marked in the
+// occurrence bitmap), first occurrences per occurrence tile and their scan,
+// then ranks.
+struct RunsOutputs {
+  uint32_t *run_key;              // or null
+  const uint32_t *grad_row;       // gathered into sorted order when non-null
+  const float *scale;             // gathered into sorted order when non-null
+  int64_t *first_indices;         // or null
+  void *unique_out;               // or null
+  int unique_source;
+  const void *values;
+  int value_bytes;
+  int64_t *unique_count;          // or null
+};
+
+template <typename K>
+int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t n, K sentinel,
+                  int use_sentinel, const RunsOutputs &o, hipStream_t s) {
+  uint32_t *head_prefix = w.scan_status;
+  uint32_t *first_prefix = w.scan_status + w.tiles;
+  head_count_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(sk, n, sentinel, use_sentinel, head_prefix);
+  scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
+  runs_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
+      sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_bits, w.head_run,
+      w.meta, head_prefix, o.run_key, o.grad_row, o.scale,
+      o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
+      w.run_grad_row, w.run_scale);
+  first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_bits, n, first_prefix);
+  scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
+  rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
+      w.head_bits, w.head_run, n, first_prefix, w.tiles, w.run_rank, o.first_indices,
+      o.unique_out, o.unique_source, o.values, o.value_bytes, o.run_key, o.unique_count);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
 int sort_passes(int bits) { return std::max(1, (bits + kRadixBits - 1) / kRadixBits); }
 
 // After prepare: sort, runs, rank.  Sorted u32 keys/vals are left in
 // w.keys[*sorted] / w.vals[*sorted].
+// scale_src: per-occurrence scale gathered into sorted order (mean divisors), or null.
 int dedup_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipStream_t s,
                int *sorted, int64_t *first_indices, void *unique_out, int unique_source,
-               const void *values, int value_bytes, int64_t *unique_count) {
+               const void *values, int value_bytes, int64_t *unique_count,
+               const float *scale_src) {
   FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, sorted));
   const uint32_t n = static_cast<uint32_t>(w.n);
   const uint32_t *sk = static_cast<const uint32_t *>(w.keys[*sorted]);
-  runs_kernel<uint32_t><<<w.tiles, kSortThreads, 0, s>>>(
-      sk, w.vals[*sorted], n, sentinel, 1, w.run_start, w.unit_first_run, w.run_of_occ, w.meta,
-      w.scan_status, w.tickets + 8, err);
-  FLARE_TRY_HIP(hipGetLastError());
-  rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
-      w.run_of_occ, n, w.scan_status + w.tiles, w.tickets + 9, w.tiles, err, w.run_rank,
-      first_indices, unique_out, unique_source, values, value_bytes, sk, w.run_start,
-      unique_count);
-  FLARE_TRY_HIP(hipGetLastError());
-  return FLARE_OK;
+  RunsOutputs o{w.run_key, w.grad_row, scale_src, first_indices, unique_out, unique_source,
+                values, value_bytes, unique_count};
+  return runs_and_rank<uint32_t>(w, sk, w.vals[*sorted], n, sentinel, 1, o, s);
 }
 
 int optimizer_mode(const flare_optimizer *opt, int *mode) {
@@ -1127,7 +1468,7 @@ int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipSt
                 const flare_optimizer *opt, int32_t norm_steps) {
   int sorted = 0;
   FLARE_TRY(dedup_rows(w, bits, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
-                       0, nullptr));
+                       0, nullptr, nullptr));
   UpdateArgs a{};
   a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
   a.sv = w.vals[sorted];
@@ -1144,6 +1485,8 @@ int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipSt
   a.dim = dim;
   a.partial = w.partial;
   a.sums = w.sums;
+  a.run_key = w.run_key;
+  a.hot_runs = w.hot_runs;
   a.out = out;
   a.table = table;
   a.s0 = s0;
@@ -1199,7 +1542,7 @@ static int scatter_common(int64_t emb_rows, int32_t dim, const int32_t *inverse,
   prepare_rows_kernel<int32_t><<<grid, 256, 0, s>>>(inverse, slots, emb_rows, 1, pad_index,
                                                    sort_passes(bits),
                                                    static_cast<uint32_t *>(w.keys[0]),
-                                                   w.run_of_occ, w.hist, err);
+                                                   w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   return reduce_rows(w, bits, sentinel, err, s, kModeRows, FLARE_FLOAT32, dim, grad,
                      grad_div == 1 ? kGradRowOcc : kGradRowDiv, grad_div, out, nullptr, nullptr,
@@ -1274,16 +1617,13 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     FLARE_TRY_HIP(hipGetLastError());
     int sorted = 0;
     FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, &sorted));
-    runs_kernel<uint32_t><<<w.tiles, kSortThreads, 0, s>>>(
-        static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n), 0u, 0,
-        w.run_start, w.unit_first_run, w.run_of_occ, w.meta, w.scan_status, w.tickets + 8, err);
-    FLARE_TRY_HIP(hipGetLastError());
-    rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
-        w.run_of_occ, static_cast<uint32_t>(n), w.scan_status + w.tiles, w.tickets + 9, w.tiles, err,
-        w.run_rank, first_indices_out, unique_out, kUniqueFromValues, values, value_bytes, nullptr,
-        w.run_start, unique_count);
-    FLARE_TRY_HIP(hipGetLastError());
-    inverse_kernel<<<grid, 256, 0, s>>>(w.run_of_occ, w.run_rank, n, inverse_out);
+    RunsOutputs o{w.run_key, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+                  values, value_bytes, unique_count};
+    FLARE_TRY(runs_and_rank<uint32_t>(w, static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted],
+                                      static_cast<uint32_t>(n), 0u, 0, o, s));
+    inverse_kernel<uint32_t><<<static_cast<int>(ceil_div(n, 256)), 256, 0, s>>>(
+        static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n),
+        w.unit_first_run, w.run_rank, inverse_out);
     FLARE_TRY_HIP(hipGetLastError());
     return FLARE_OK;
   }
@@ -1294,16 +1634,13 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   FLARE_TRY(run_sort<uint64_t>(w, bits, err, s, &sorted));
-  runs_kernel<uint64_t><<<w.tiles, kSortThreads, 0, s>>>(
-      static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n), 0ull, 0,
-      w.run_start, w.unit_first_run, w.run_of_occ, w.meta, w.scan_status, w.tickets + 8, err);
-  FLARE_TRY_HIP(hipGetLastError());
-  rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
-      w.run_of_occ, static_cast<uint32_t>(n), w.scan_status + w.tiles, w.tickets + 9, w.tiles, err,
-      w.run_rank, first_indices_out, unique_out, kUniqueFromValues, values, value_bytes, nullptr,
-      w.run_start, unique_count);
-  FLARE_TRY_HIP(hipGetLastError());
-  inverse_kernel<<<grid, 256, 0, s>>>(w.run_of_occ, w.run_rank, n, inverse_out);
+  RunsOutputs o{nullptr, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+                values, value_bytes, unique_count};
+  FLARE_TRY(runs_and_rank<uint64_t>(w, static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted],
+                                    static_cast<uint32_t>(n), 0ull, 0, o, s));
+  inverse_kernel<uint64_t><<<static_cast<int>(ceil_div(n, 256)), 256, 0, s>>>(
+      static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted], static_cast<uint32_t>(n),
+      w.unit_first_run, w.run_rank, inverse_out);
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }
@@ -1366,7 +1703,7 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
   FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
   const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n, 256), 2048));
   prepare_rows_kernel<int64_t><<<grid, 256, 0, s>>>(keys, n, rows, 0, 0, sort_passes(bits),
-                                                   static_cast<uint32_t *>(w.keys[0]), w.run_of_occ,
+                                                   static_cast<uint32_t *>(w.keys[0]),
                                                    w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   return reduce_rows(w, bits, sentinel, err, s, mode, value_dtype, dim, grad, kGradRowOcc, 1,
@@ -1427,17 +1764,15 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.run_of_occ,
-        w.hist, err);
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.run_of_occ,
-        w.hist, err);
+        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   return dedup_rows(w, bits, sentinel, err, s, &sorted, first_indices_out, unique_out,
-                    unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count);
+                    unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count, aux);
 }
 
 extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
@@ -1475,13 +1810,19 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   a.grad = pooled_grad;
   a.grad_mode = kGradRowArray;
   a.grad_row = w.grad_row;
+  a.sorted_grad_row = w.sorted_grad_row;
   a.scale_mode = pooling == FLARE_POOL_WEIGHTED ? kScaleMul : (pooling == FLARE_POOL_MEAN ? kScaleDiv : kScaleNone);
   a.scale = pooling == FLARE_POOL_WEIGHTED ? weights : w.aux;
+  a.sorted_scale = pooling == FLARE_POOL_MEAN ? w.sorted_scale : nullptr;
+  a.run_grad_row = w.run_grad_row;
+  a.run_scale = pooling == FLARE_POOL_MEAN ? w.run_scale : nullptr;
   a.use_norm = normalization_steps != 1;
   a.norm = static_cast<float>(normalization_steps);
   a.dim = dim;
   a.partial = w.partial;
   a.sums = w.sums;
+  a.run_key = w.run_key;
+  a.hot_runs = w.hot_runs;
   a.out = grad_out;
   a.table = table;
   a.s0 = state0;

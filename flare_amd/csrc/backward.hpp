@@ -18,8 +18,6 @@ constexpr int kRadix = 1 << kRadixBits;
 // a key's occurrences inside one unit are summed sequentially and the unit
 // partials of a key that spans several units are folded left to right.
 constexpr int kReduceUnit = 64;
-constexpr uint32_t kInvalidRun = 0x7fffffffu;
-constexpr uint32_t kHeadBit = 0x80000000u;
 constexpr int64_t kMaxOccurrences = (int64_t{1} << 30) - 1;
 // Blocks add their digit histograms into one of kHistCopies copies (by block
 // index) to spread same-address atomics; a radix pass sums the copies.
@@ -32,19 +30,26 @@ struct Workspace {
   // zero-initialized region (first)
   uint32_t *hist;         // [kHistCopies][kMaxPasses][kRadix] digit histograms
   uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
-  uint32_t *meta;         // [4]: nvalid, unique count
+  uint32_t *meta;         // [4]: nvalid, unique count, hot-key count
   uint32_t *sort_status;  // [8][sort_tiles][kRadix]
   uint32_t *scan_status;  // [2][tiles]
+  uint32_t *head_bits;    // [ceil(n/32)] bit o set: occurrence o is its key's first
   size_t zero_bytes;
   // not initialized
   void *keys[2];
   uint32_t *vals[2];
   uint32_t *grad_row;     // [n] (CSR gradient row of each occurrence)
   float *aux;             // [n] (mean-pooling divisor of each occurrence)
-  uint32_t *run_of_occ;   // [n]
+  uint32_t *sorted_grad_row;  // [n] grad_row of the occurrence at each sorted position
+  float *sorted_scale;        // [n] aux of the occurrence at each sorted position
+  uint32_t *run_grad_row;     // [n] sorted_grad_row at each key's first position
+  float *run_scale;           // [n] sorted_scale at each key's first position
+  uint32_t *head_run;     // [n] run of each first occurrence (where head_bits is set)
   uint32_t *run_start;    // [n + 1]
   uint32_t *run_rank;     // [n]
+  uint32_t *run_key;      // [n] key of each run (32-bit sorts)
   uint32_t *unit_first_run;  // [units]
+  uint32_t *hot_runs;     // [units] keys whose partials apply_kernel does not fold
   float *partial;         // [units][2][dim]
   float *sums;            // [n][dim] per-key gradient sums (optimizer modes)
   size_t total_bytes;

@@ -134,6 +134,25 @@ __device__ __forceinline__ void store_from_f32(typename Tag::elem *p, const floa
   *reinterpret_cast<R *>(p) = raw;
 }
 
+// Like store_from_f32, with a nontemporal hint for 16-byte vectors: for
+// outputs that this library does not read back (the pooled rows), so they
+// stream past L2 instead of evicting rows that later kernels reuse.
+template <typename Tag, int VEC>
+__device__ __forceinline__ void store_from_f32_stream(typename Tag::elem *p, const float (&in)[VEC]) {
+  using E = typename Tag::elem;
+  if constexpr (sizeof(E) * VEC == 16) {
+    E tmp[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) tmp[i] = Tag::from_f32(in[i]);
+    typedef unsigned int U4 __attribute__((ext_vector_type(4)));
+    U4 raw;
+    __builtin_memcpy(&raw, tmp, sizeof(raw));
+    __builtin_nontemporal_store(raw, reinterpret_cast<U4 *>(p));
+  } else {
+    store_from_f32<Tag, VEC>(p, in);
+  }
+}
+
 template <int VEC>
 __device__ __forceinline__ void load_f32(const float *p, float (&out)[VEC]) {
   using R = typename Raw<VEC * 4>::type;

@@ -67,7 +67,7 @@ struct PooledArgs {
   int *err;
 };
 
-constexpr int kBagsPerGroup = 4;
+constexpr int kBagsPerGroup = 8;
 
 // Resolve one id to a table row (or -1 for a pad / out-of-range slot).
 template <bool kCsr, typename IdT>
@@ -86,13 +86,15 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
   }
 }
 
-// A group of G lanes pools kBagsPerGroup consecutive bags; lane l holds L
-// vectors of VEC elements at columns (q*G + l)*VEC.  The group streams the
-// ids of its bags as one run (G ids per lane-parallel load), gathers rows
-// kDepth at a time regardless of bag boundaries (packed, so four rows of
-// loads are in flight per lane), accumulates in occurrence order, and stores
-// a bag's pooled row when the stream passes the bag's end.  One-id bags thus
-// cost a single round of dependent row loads per four bags.
+// A block pools kBagsPerBlock consecutive OUTPUT rows (CSR: output row
+// o = b*T + t is bag t*B + b), so its stores form one contiguous range.  Each
+// bag's [begin, end) and table base are staged in LDS.  A group of G lanes
+// pools kBagsPerGroup of those bags: it streams their ids as one virtual run
+// (G ids per lane-parallel load, each lane finding its bag from the running
+// lengths), gathers rows kDepth at a time regardless of bag boundaries
+// (packed, so four rows of loads are in flight per lane), accumulates in
+// occurrence order, and stores a bag's pooled row when the stream passes the
+// bag's end.  Lane l holds L vectors of VEC elements at columns (q*G + l)*VEC.
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   using E = typename Tag::elem;
@@ -100,29 +102,49 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
   constexpr int kDepth = 4;
-  __shared__ int64_t s_off[kBagsPerBlock + 1];
+  __shared__ int64_t s_begin[kBagsPerBlock];
+  __shared__ int64_t s_len[kBagsPerBlock];
+  __shared__ int64_t s_lo[kBagsPerBlock];
+  __shared__ int64_t s_rows[kBagsPerBlock];
 
   const int lane = threadIdx.x % G;
   const int group = threadIdx.x / G;
-  const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * kBagsPerBlock;
-  const int64_t nbags = (a.bags - bag0) < kBagsPerBlock ? (a.bags - bag0) : kBagsPerBlock;
+  const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kBagsPerBlock;
+  const int64_t nout = (a.bags - o0) < kBagsPerBlock ? (a.bags - o0) : kBagsPerBlock;
 
-  for (int i = threadIdx.x; i <= nbags; i += kThreads) {
+  for (int i = threadIdx.x; i < nout; i += kThreads) {
+    const int64_t o = o0 + i;
     if constexpr (kCsr) {
-      const int64_t o = a.offsets[bag0 + i];
-      s_off[i] = o < 0 ? 0 : (o > a.num_ids ? a.num_ids : o);
+      const int64_t b = o / a.num_tables;
+      const int64_t t = o - b * a.num_tables;
+      const int64_t bag = t * a.batch + b;
+      int64_t lo = a.offsets[bag];
+      int64_t hi = a.offsets[bag + 1];
+      lo = lo < 0 ? 0 : (lo > a.num_ids ? a.num_ids : lo);
+      hi = hi < lo ? lo : (hi > a.num_ids ? a.num_ids : hi);  // decreasing offsets pool nothing
+      s_begin[i] = lo;
+      s_len[i] = hi - lo;
+      const int64_t base = a.row_base[t];
+      s_lo[i] = base;
+      s_rows[i] = a.row_base[t + 1] - base;
     } else {
-      s_off[i] = (bag0 + i) * a.max_elements;
+      s_begin[i] = o * a.max_elements;
+      s_len[i] = a.max_elements;
+      s_lo[i] = 0;
+      s_rows[i] = a.table_rows;
     }
   }
   __syncthreads();
 
-  const int lb0 = group * kBagsPerGroup;  // first bag of this group, block-local
-  const int nb = static_cast<int>(nbags - lb0 < kBagsPerGroup ? nbags - lb0 : kBagsPerGroup);
+  const int lb0 = group * kBagsPerGroup;  // first output row of this group, block-local
+  const int nb = static_cast<int>(nout - lb0 < kBagsPerGroup ? nout - lb0 : kBagsPerGroup);
   if (nb <= 0) return;
-  const int64_t s = s_off[lb0];
-  int64_t e = s_off[lb0 + nb];
-  if (e < s) e = s;  // decreasing offsets: pool nothing rather than read out of range
+  // running start of each bag in the group's virtual id sequence
+  int64_t pre[kBagsPerGroup + 1];
+  pre[0] = 0;
+#pragma unroll
+  for (int k = 0; k < kBagsPerGroup; ++k) pre[k + 1] = pre[k] + (k < nb ? s_len[lb0 + k] : 0);
+  const int64_t total = pre[kBagsPerGroup];
 
   const E *table = static_cast<const E *>(a.table);
   E *out = static_cast<E *>(a.out);
@@ -140,12 +162,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
     int cur = 0;  // bag being pooled, group-local
 
     auto flush = [&]() {
-      const int64_t bag = bag0 + lb0 + cur;
-      int64_t out_row = bag;
-      if constexpr (kCsr) {
-        const int64_t t = bag / a.batch;
-        out_row = (bag - t * a.batch) * a.num_tables + t;
-      }
+      const int64_t out_row = o0 + lb0 + cur;
       const float div = static_cast<float>(count > 0 ? count : 1);
 #pragma unroll
       for (int q = 0; q < L; ++q) {
@@ -154,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
           for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
         }
         const int col = c0 + (q * G + lane) * VEC;
-        if (col < D) store_from_f32<Tag, VEC>(out + out_row * D + col, acc[q]);
+        if (col < D) store_from_f32_stream<Tag, VEC>(out + out_row * D + col, acc[q]);
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
       }
@@ -162,24 +179,21 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
       ++cur;
     };
 
-    for (int64_t base = s; base < e; base += G) {
+    for (int64_t base = 0; base < total; base += G) {
       int64_t my_row = -1;
       float my_w = 1.0f;
-      const int64_t i = base + lane;
-      if (i < e) {
-        int64_t lo = 0, hi = a.table_rows;
-        if constexpr (kCsr) {
-          int k = 0;  // bag of position i within the group
+      const int64_t vpos = base + lane;
+      if (vpos < total) {
+        int k = 0;  // bag of this virtual position within the group
 #pragma unroll
-          for (int j = 1; j < kBagsPerGroup; ++j) k += (j < nb && i >= s_off[lb0 + j]) ? 1 : 0;
-          const int64_t t = (bag0 + lb0 + k) / a.batch;
-          lo = a.row_base[t];
-          hi = a.row_base[t + 1];
-        }
-        my_row = resolve_row<kCsr, IdT>(a, i, lo, hi);
+        for (int j = 1; j < kBagsPerGroup; ++j) k += (vpos >= pre[j]) ? 1 : 0;
+        const int lb = lb0 + k;
+        const int64_t i = s_begin[lb] + (vpos - pre[k]);
+        const int64_t lo = s_lo[lb];
+        my_row = resolve_row<kCsr, IdT>(a, i, lo, lo + s_rows[lb]);
         if (weighted) my_w = a.weights[i];
       }
-      const int n = (e - base) < G ? static_cast<int>(e - base) : G;
+      const int n = (total - base) < G ? static_cast<int>(total - base) : G;
       for (int k = 0; k < n; k += kDepth) {
         R raw[kDepth][L];
         int64_t rows[kDepth];
@@ -201,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
         for (int h = 0; h < kDepth; ++h) {
           if (k + h >= n) break;
           const int64_t p = base + k + h;
-          while (cur < nb - 1 && p >= s_off[lb0 + cur + 1]) flush();
+          while (cur < nb - 1 && p >= pre[cur + 1]) flush();
           if (rows[h] < 0) continue;
           ++count;
 #pragma unroll
