@@ -3,18 +3,23 @@
 // optimizer row update.
 //
 // Kernel sequence of one call (all on the caller's stream):
-//   zero      clear histograms, tile tickets, look-back status, counters
-//   prepare   build the 32/64-bit sort key of every occurrence (invalid ->
-//             sentinel) and the digit histograms of every radix pass
-//   onesweep  one launch per 8-bit digit: stable in-tile ranking with wave64
-//             ballots, decoupled look-back across tiles, LDS-staged scatter
-//   runs      segment heads of the sorted keys -> run ids (chained scan)
-//   rank      first-occurrence order: scan of "is first occurrence" flags in
-//             occurrence order -> unique / first_indices / run -> rank
-//   update    per 64-position unit: sequential fp32 sum of each key's
-//             gradient rows in occurrence order, unit partials folded left to
-//             right by the last unit to finish, then the optimizer update
-//             (or the reduced gradient) written once per unique key
+//   zero        clear histograms, tile tickets, look-back status, counters and
+//               the first-occurrence bitmap
+//   prepare     build the 32/64-bit sort key of every occurrence (invalid ->
+//               sentinel) and the digit histograms of every radix pass
+//   onesweep    one launch per 8-bit digit: stable in-tile ranking with wave64
+//               ballots, decoupled look-back across tiles, LDS-staged scatter
+//   head_count  key heads per tile of sorted keys, scanned by scan_counts
+//   runs        run ids, run starts / keys, each key's first occurrence set in
+//               the bitmap, gradient rows gathered into sorted order
+//   first_count first occurrences per tile of occurrences, scanned
+//   rank        first-occurrence order: unique / first_indices / run -> rank
+//   sums        long keys: per 64-position unit, sequential fp32 sums of the
+//               key's gradient rows in occurrence order (per-key sums, or
+//               unit partials for keys that span units)
+//   fold        keys spanning many units: one block folds the unit partials
+//   apply       per key: short keys summed here; then the optimizer update
+//               (or the reduced gradient) written once per unique key
 #include "backward.hpp"
 
 #include <algorithm>

@@ -12,6 +12,28 @@ Every public function names the reference lines it follows.  Where the
 reference has no definition (bf16 storage, mean / weighted pooling, row-wise
 Adagrad, the deterministic reduction order) the docstring says so and states
 the closed form used instead.
+
+How each part is pinned (tests/test_oracle.py, tests/test_golden.py):
+
+* unique_first_occurrence_*: the reference's literal vectors
+  (tests/runtime/test_sparse_input_resources.py:77-123) and a dict brute force.
+* gather / gather_pooled (sum): the reference's known answers
+  (tests/kernels/test_sparse_embedding_backend.py:78-89,144-183,225-233) and
+  the audit restatement padded[inverse].sum(axis=2).
+* mean / weighted pooling, gather_pooled_csr: closed forms and the CSR ==
+  materialized-padded identity.
+* bf16 rounding: torch.bfloat16 casts.
+* scatter / scatter_pooled / segment_sums: the reference's own test cases and
+  np.add.at; one-unit keys equal the plain slot-order sum bit for bit.
+* adam_update: the reference's two-step known answer and a float64 textbook.
+* rowwise_adagrad_update: the optax closed form it reduces to at D == 1 and
+  the row mean of squares.
+* sgd_update: the flush-window known answer.
+
+Parity unpinned (only the external sparse_embedding store defines these, and
+it is not available here): the rounding of updated fp16 / bf16 rows (RNE is
+used), and the division of the summed gradient by normalization_steps for
+Adam and row-wise Adagrad (pinned only for SGD by the flush-window test).
 """
 
 from __future__ import annotations
