@@ -51,12 +51,15 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     off = align_up(off + bytes);
     return at;
   };
-  const size_t o_hist = take(static_cast<size_t>(kHistCopies) * kMaxPasses * kRadix * 4);
+  const size_t o_hist = take(static_cast<size_t>(kHistCopies) * kMaxPasses * kMaxRadix * 4);
   const size_t o_tickets = take(16 * 4);
   const size_t o_meta = take(4 * 4);
-  const size_t o_sort_status = take(static_cast<size_t>(8) * w.sort_tiles * kRadix * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
   const size_t o_head_bits = take(static_cast<size_t>(ceil_div(std::max<int64_t>(n, 1), 32)) * 4);
+  // per tile: every plan's passes x 2^digit bits (8 x 256 for 64-bit keys, 3 x 1024 at most for 32-bit)
+  const size_t status_per_tile = std::max<size_t>(kMaxPasses * 256, 3 * kMaxRadix);
+  const size_t o_sort_status = take(status_per_tile * w.sort_tiles * 4);
+  w.sort_status_offset = o_sort_status;
   w.zero_bytes = off;
   const size_t o_k0 = take(un * key_bytes);
   const size_t o_k1 = take(un * key_bytes);
@@ -107,6 +110,22 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   return w;
 }
 
+RadixPlan radix_plan(int bits, int key_bytes) {
+  const int p8 = std::max(1, (bits + 7) / 8);
+  if (key_bytes == 4) {
+    for (int d = 9; d <= kMaxDigitBits; ++d) {
+      const int p = std::max(1, (bits + d - 1) / d);
+      if (p < p8) return {d, p};
+    }
+  }
+  return {8, p8};
+}
+
+size_t zero_bytes_for(const Workspace &w, const RadixPlan &plan) {
+  const size_t status = static_cast<size_t>(plan.passes) * w.sort_tiles * (size_t{1} << plan.digit_bits) * 4;
+  return std::min(w.zero_bytes, align_up(w.sort_status_offset + status));
+}
+
 namespace {
 
 // ----------------------------------------------------------------------------
@@ -134,18 +153,20 @@ int launch_zero(void *p, size_t bytes, hipStream_t s) {
 // prepare: keys + histograms
 // ----------------------------------------------------------------------------
 template <typename K>
-__device__ __forceinline__ void add_histograms(uint32_t *s_hist, K key, int passes) {
+__device__ __forceinline__ void add_histograms(uint32_t *s_hist, K key, int passes, int digit) {
+  const uint32_t mask = (1u << digit) - 1;
   for (int p = 0; p < passes; ++p) {
-    const uint32_t d = static_cast<uint32_t>(key >> (p * kRadixBits)) & (kRadix - 1);
-    atomicAdd(&s_hist[p * kRadix + d], 1u);
+    const uint32_t d = static_cast<uint32_t>(key >> (p * digit)) & mask;
+    atomicAdd(&s_hist[(p << digit) + d], 1u);
   }
 }
 
-__device__ __forceinline__ void flush_histograms(const uint32_t *s_hist, uint32_t *hist, int passes) {
-  uint32_t *copy = hist + static_cast<size_t>(blockIdx.x % kHistCopies) * kMaxPasses * kRadix;
-  for (int i = threadIdx.x; i < passes * kRadix; i += blockDim.x) {
+__device__ __forceinline__ void flush_histograms(const uint32_t *s_hist, uint32_t *hist, int passes,
+                                                 int digit) {
+  uint32_t *copy = hist + static_cast<size_t>(blockIdx.x % kHistCopies) * kMaxPasses * kMaxRadix;
+  for (int i = threadIdx.x; i < (passes << digit); i += blockDim.x) {
     const uint32_t c = s_hist[i];
-    if (c) atomicAdd(&copy[i], c);
+    if (c) atomicAdd(&copy[(i >> digit) * kMaxRadix + (i & ((1 << digit) - 1))], c);
   }
 }
 
@@ -153,7 +174,7 @@ __device__ __forceinline__ void flush_histograms(const uint32_t *s_hist, uint32_
 __device__ __forceinline__ uint32_t digit_total(const uint32_t *hist, int pass, int d) {
   uint32_t sum = 0;
 #pragma unroll
-  for (int c = 0; c < kHistCopies; ++c) sum += hist[(static_cast<size_t>(c) * kMaxPasses + pass) * kRadix + d];
+  for (int c = 0; c < kHistCopies; ++c) sum += hist[(static_cast<size_t>(c) * kMaxPasses + pass) * kMaxRadix + d];
   return sum;
 }
 
@@ -162,11 +183,11 @@ __device__ __forceinline__ uint32_t digit_total(const uint32_t *hist, int pass, 
 template <typename SrcT>
 __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restrict__ src, int64_t n,
                                                           int64_t key_limit, int has_pad,
-                                                          int64_t pad, int passes,
+                                                          int64_t pad, int passes, int digit,
                                                           uint32_t *__restrict__ keys,
                                                           uint32_t *__restrict__ hist, int *err) {
-  __shared__ uint32_t s_hist[4 * kRadix];
-  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  __shared__ uint32_t s_hist[kMaxHistBins];
+  for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
   __syncthreads();
   const uint32_t sentinel = static_cast<uint32_t>(key_limit);
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
@@ -180,10 +201,10 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
       }
     }
     keys[i] = k;
-    add_histograms(s_hist, k, passes);
+    add_histograms(s_hist, k, passes, digit);
   }
   __syncthreads();
-  flush_histograms(s_hist, hist, passes);
+  flush_histograms(s_hist, hist, passes, digit);
 }
 
 // Keys from CSR bags (table-major, bag k = t*batch + b).  The block's bag
@@ -201,11 +222,11 @@ template <typename IdT>
 __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
-    int64_t key_limit, int passes, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
+    int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
     float *__restrict__ aux, uint32_t *__restrict__ hist, int *err) {
-  __shared__ uint32_t s_hist[4 * kRadix];
+  __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
-  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
   const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * bags_per_block;
   const int nb = static_cast<int>(std::min<int64_t>(bags_per_block, bags - bag0));
   for (int i = threadIdx.x; i <= nb; i += 256) {
@@ -241,10 +262,10 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     keys[i] = k;
     grad_row[i] = static_cast<uint32_t>(b * num_tables + t);
     if (aux) aux[i] = static_cast<float>(s_off[lo + 1] - s_off[lo]);
-    add_histograms(s_hist, k, passes);
+    add_histograms(s_hist, k, passes, digit);
   }
   __syncthreads();
-  flush_histograms(s_hist, hist, passes);
+  flush_histograms(s_hist, hist, passes, digit);
 }
 
 // Keys for generic dedup: (value - minimum) as unsigned, 32 or 64 bits.
@@ -252,13 +273,13 @@ template <typename SrcT, typename K>
 __global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__restrict__ src,
                                                              int64_t n,
                                                              const uint64_t *__restrict__ minimum,
-                                                             int passes, K *__restrict__ keys,
+                                                             int passes, int digit, K *__restrict__ keys,
                                                              uint32_t *__restrict__ hist) {
   // minimum != nullptr: keys are mapped to their order-preserving unsigned
   // image and offset by the measured minimum; otherwise the caller promised
   // 0 <= key < bound and the raw value is the key.
-  __shared__ uint32_t s_hist[8 * kRadix];
-  for (int i = threadIdx.x; i < passes * kRadix; i += 256) s_hist[i] = 0;
+  __shared__ uint32_t s_hist[kMaxHistBins];
+  for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
   __syncthreads();
   const uint64_t lo = minimum ? *minimum : 0;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) {
@@ -271,10 +292,10 @@ __global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__rest
     }
     const K k = static_cast<K>(ord - lo);
     keys[i] = k;
-    add_histograms(s_hist, k, passes);
+    add_histograms(s_hist, k, passes, digit);
   }
   __syncthreads();
-  flush_histograms(s_hist, hist, passes);
+  flush_histograms(s_hist, hist, passes, digit);
 }
 
 // Order-preserving unsigned image of the keys: min and max (for the bit width).
@@ -311,14 +332,15 @@ __global__ void init_minmax_kernel(unsigned long long *out) {
 // ----------------------------------------------------------------------------
 // onesweep radix pass (stable)
 // ----------------------------------------------------------------------------
-template <typename K>
+template <typename K, int DIGIT>
 __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     const K *__restrict__ kin, const uint32_t *__restrict__ vin, K *__restrict__ kout,
     uint32_t *__restrict__ vout, uint32_t n, int pass, const uint32_t *__restrict__ hist,
     uint32_t *status, uint32_t *ticket, int *err) {
   constexpr int kWaves = kOneThreads / 64;
+  constexpr int kRadix = 1 << DIGIT;
   static_assert(kOneThreads >= kRadix, "one thread per digit");
-  const int shift = pass * kRadixBits;
+  const int shift = pass * DIGIT;
   __shared__ uint32_t s_tile;
   __shared__ uint32_t s_wcnt[kWaves][kRadix];
   __shared__ uint32_t s_tile_start[kRadix];
@@ -363,7 +385,7 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     const uint32_t d = valid ? (static_cast<uint32_t>(key[k] >> shift) & (kRadix - 1)) : 0;
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < kRadixBits; ++b) {
+    for (int b = 0; b < DIGIT; ++b) {
       const bool bit = (d >> b) & 1u;
       const uint64_t bb = __ballot(bit);
       peers &= bit ? bb : ~bb;
@@ -1355,16 +1377,15 @@ int launch_update(int mode, int dtype, const UpdateArgs &a, const Shape &sh, hip
 
 // Sort keys[0]/implicit iota by the low `bits` bits; returns the buffer index
 // holding the result (0 or 1).
-template <typename K>
-int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result) {
-  const int passes = std::max(1, (bits + kRadixBits - 1) / kRadixBits);
+template <typename K, int DIGIT>
+int run_passes(const Workspace &w, int passes, int *err, hipStream_t s, int *result) {
   const uint32_t n = static_cast<uint32_t>(w.n);
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
-    onesweep_kernel<K><<<w.sort_tiles, kOneThreads, 0, s>>>(
+    onesweep_kernel<K, DIGIT><<<w.sort_tiles, kOneThreads, 0, s>>>(
         static_cast<const K *>(w.keys[cur]), p == 0 ? nullptr : w.vals[cur],
         static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p,
-        w.hist, w.sort_status + static_cast<size_t>(p) * w.sort_tiles * kRadix,
+        w.hist, w.sort_status + (static_cast<size_t>(p) * w.sort_tiles << DIGIT),
         w.tickets + p, err);
     FLARE_TRY_HIP(hipGetLastError());
     cur ^= 1;
@@ -1372,6 +1393,16 @@ int run_sort(const Workspace &w, int bits, int *err, hipStream_t s, int *result)
   *result = cur;
   return FLARE_OK;
 }
+
+template <typename K>
+int run_sort(const Workspace &w, const RadixPlan &plan, int *err, hipStream_t s, int *result) {
+  if constexpr (sizeof(K) == 4) {
+    if (plan.digit_bits == 9) return run_passes<K, 9>(w, plan.passes, err, s, result);
+    if (plan.digit_bits == 10) return run_passes<K, 10>(w, plan.passes, err, s, result);
+  }
+  return run_passes<K, 8>(w, plan.passes, err, s, result);
+}
+
 
 // Runs and first-occurrence ranks of sorted keys: head counts per tile and
 // their scan, runs (run ids; each key's first occurrence marked in the
@@ -1410,16 +1441,14 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
   return FLARE_OK;
 }
 
-int sort_passes(int bits) { return std::max(1, (bits + kRadixBits - 1) / kRadixBits); }
-
 // After prepare: sort, runs, rank.  Sorted u32 keys/vals are left in
 // w.keys[*sorted] / w.vals[*sorted].
 // scale_src: per-occurrence scale gathered into sorted order (mean divisors), or null.
-int dedup_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipStream_t s,
+int dedup_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int *err, hipStream_t s,
                int *sorted, int64_t *first_indices, void *unique_out, int unique_source,
                const void *values, int value_bytes, int64_t *unique_count,
                const float *scale_src) {
-  FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, sorted));
+  FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, sorted));
   const uint32_t n = static_cast<uint32_t>(w.n);
   const uint32_t *sk = static_cast<const uint32_t *>(w.keys[*sorted]);
   RunsOutputs o{w.run_key, w.grad_row, scale_src, first_indices, unique_out, unique_source,
@@ -1467,12 +1496,12 @@ int check_workspace(const Workspace &need, size_t have) {
 bool vec4_ok(const void *p) { return aligned(p, 16); }
 
 // Shared tail of the keyed-row entry points (scatter, scatter_pooled, sparse_update).
-int reduce_rows(const Workspace &w, int bits, uint32_t sentinel, int *err, hipStream_t s, int mode,
+int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int *err, hipStream_t s, int mode,
                 int dtype, int dim, const float *grad, int grad_mode, uint32_t grad_div,
                 float *out, void *table, float *s0, float *s1, int32_t *step,
                 const flare_optimizer *opt, int32_t norm_steps) {
   int sorted = 0;
-  FLARE_TRY(dedup_rows(w, bits, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
+  FLARE_TRY(dedup_rows(w, plan, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
                        0, nullptr, nullptr));
   UpdateArgs a{};
   a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
@@ -1541,15 +1570,15 @@ static int scatter_common(int64_t emb_rows, int32_t dim, const int32_t *inverse,
   int *err = device_error_word(&st);
   if (!err) return st;
   const uint32_t sentinel = static_cast<uint32_t>(emb_rows);
-  const int bits = bits_for(sentinel);
-  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const RadixPlan plan = radix_plan(bits_for(sentinel), 4);
+  FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
   const int grid = static_cast<int>(std::min<int64_t>(ceil_div(slots, 256), 2048));
   prepare_rows_kernel<int32_t><<<grid, 256, 0, s>>>(inverse, slots, emb_rows, 1, pad_index,
-                                                   sort_passes(bits),
+                                                   plan.passes, plan.digit_bits,
                                                    static_cast<uint32_t *>(w.keys[0]),
                                                    w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
-  return reduce_rows(w, bits, sentinel, err, s, kModeRows, FLARE_FLOAT32, dim, grad,
+  return reduce_rows(w, plan, sentinel, err, s, kModeRows, FLARE_FLOAT32, dim, grad,
                      grad_div == 1 ? kGradRowOcc : kGradRowDiv, grad_div, out, nullptr, nullptr,
                      nullptr, nullptr, nullptr, 1);
 }
@@ -1611,17 +1640,18 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     minimum = reinterpret_cast<const uint64_t *>(mm);
   }
   const int bits = bits_for(range);
-  const int passes = sort_passes(bits);
   const int value_bytes = sizeof(SrcT);
   if (bits <= 32) {
     // same base pointer, 4-byte keys
     Workspace w = layout_workspace(workspace, n, 4, 1, false, false, false);
-    FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
-    prepare_generic_kernel<SrcT, uint32_t><<<grid, 256, 0, s>>>(values, n, minimum, passes,
+    const RadixPlan plan = radix_plan(bits, 4);
+    FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
+    prepare_generic_kernel<SrcT, uint32_t><<<grid, 256, 0, s>>>(values, n, minimum, plan.passes,
+                                                                plan.digit_bits,
                                                                 static_cast<uint32_t *>(w.keys[0]), w.hist);
     FLARE_TRY_HIP(hipGetLastError());
     int sorted = 0;
-    FLARE_TRY(run_sort<uint32_t>(w, bits, err, s, &sorted));
+    FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, &sorted));
     RunsOutputs o{w.run_key, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                   values, value_bytes, unique_count};
     FLARE_TRY(runs_and_rank<uint32_t>(w, static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted],
@@ -1633,12 +1663,14 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     return FLARE_OK;
   }
   Workspace w = w8;
-  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
-  prepare_generic_kernel<SrcT, uint64_t><<<grid, 256, 0, s>>>(values, n, minimum, passes,
+  const RadixPlan plan = radix_plan(bits, 8);
+  FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
+  prepare_generic_kernel<SrcT, uint64_t><<<grid, 256, 0, s>>>(values, n, minimum, plan.passes,
+                                                              plan.digit_bits,
                                                               static_cast<uint64_t *>(w.keys[0]), w.hist);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
-  FLARE_TRY(run_sort<uint64_t>(w, bits, err, s, &sorted));
+  FLARE_TRY(run_sort<uint64_t>(w, plan, err, s, &sorted));
   RunsOutputs o{nullptr, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                 values, value_bytes, unique_count};
   FLARE_TRY(runs_and_rank<uint64_t>(w, static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted],
@@ -1704,14 +1736,14 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
   if (!err) return st;
   hipStream_t s = as_stream(stream);
   const uint32_t sentinel = static_cast<uint32_t>(rows);
-  const int bits = bits_for(sentinel);
-  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const RadixPlan plan = radix_plan(bits_for(sentinel), 4);
+  FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
   const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n, 256), 2048));
-  prepare_rows_kernel<int64_t><<<grid, 256, 0, s>>>(keys, n, rows, 0, 0, sort_passes(bits),
+  prepare_rows_kernel<int64_t><<<grid, 256, 0, s>>>(keys, n, rows, 0, 0, plan.passes, plan.digit_bits,
                                                    static_cast<uint32_t *>(w.keys[0]),
                                                    w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
-  return reduce_rows(w, bits, sentinel, err, s, mode, value_dtype, dim, grad, kGradRowOcc, 1,
+  return reduce_rows(w, plan, sentinel, err, s, mode, value_dtype, dim, grad, kGradRowOcc, 1,
                      nullptr, table, state0, state1, step, optimizer, normalization_steps);
 }
 
@@ -1761,22 +1793,22 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   int *err = device_error_word(&st);
   if (!err) return st;
   const uint32_t sentinel = static_cast<uint32_t>(rows);
-  const int bits = bits_for(sentinel);
-  FLARE_TRY(launch_zero(workspace, w.zero_bytes, s));
+  const RadixPlan plan = radix_plan(bits_for(sentinel), 4);
+  FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
   const int bpb = prep_bags_per_block(bags);
   const int pgrid = static_cast<int>(ceil_div(bags, bpb));
   float *aux = pooling == FLARE_POOL_MEAN ? w.aux : nullptr;
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        sort_passes(bits), static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
-  return dedup_rows(w, bits, sentinel, err, s, &sorted, first_indices_out, unique_out,
+  return dedup_rows(w, plan, sentinel, err, s, &sorted, first_indices_out, unique_out,
                     unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count, aux);
 }
 
@@ -1802,8 +1834,7 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   int st = FLARE_OK;
   int *err = device_error_word(&st);
   if (!err) return st;
-  const int bits = bits_for(static_cast<uint32_t>(rows));
-  const int sorted = sort_passes(bits) & 1;  // buffer holding the sorted pairs
+  const int sorted = radix_plan(bits_for(static_cast<uint32_t>(rows)), 4).passes & 1;  // buffer holding the sorted pairs
   UpdateArgs a{};
   a.sk = static_cast<const uint32_t *>(w.keys[sorted]);
   a.sv = w.vals[sorted];

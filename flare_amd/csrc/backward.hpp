@@ -12,8 +12,12 @@ constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 occurrences per ti
 constexpr int kOneThreads = 1024;
 constexpr int kOneItems = 8;
 constexpr int kOneTile = kOneThreads * kOneItems;
-constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;
+// Digits of 8, 9 or 10 bits (chosen per call from the key width, so that
+// 25-27-bit rows sort in 3 passes instead of 4); 64-bit keys use 8.
+constexpr int kMaxDigitBits = 10;
+constexpr int kMaxRadix = 1 << kMaxDigitBits;
+// LDS histogram bins of the prepare kernels: passes x 2^digit bits.
+constexpr int kMaxHistBins = 3 * kMaxRadix;
 // Sorted positions are reduced in units of kReduceUnit consecutive positions;
 // a key's occurrences inside one unit are summed sequentially and the unit
 // partials of a key that spans several units are folded left to right.
@@ -28,13 +32,14 @@ constexpr uint32_t kNoRun = 0xffffffffu;
 // Where every array of one call lives inside the caller's workspace.
 struct Workspace {
   // zero-initialized region (first)
-  uint32_t *hist;         // [kHistCopies][kMaxPasses][kRadix] digit histograms
+  uint32_t *hist;         // [kHistCopies][kMaxPasses][kMaxRadix] digit histograms
   uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
   uint32_t *meta;         // [4]: nvalid, unique count, hot-key count
-  uint32_t *sort_status;  // [8][sort_tiles][kRadix]
+  uint32_t *sort_status;  // [passes][sort_tiles][2^digit bits] (last in the zeroed region)
   uint32_t *scan_status;  // [2][tiles]
   uint32_t *head_bits;    // [ceil(n/32)] bit o set: occurrence o is its key's first
-  size_t zero_bytes;
+  size_t zero_bytes;      // whole zeroed region (sort status sized for the widest plan)
+  size_t sort_status_offset;
   // not initialized
   void *keys[2];
   uint32_t *vals[2];
@@ -59,6 +64,16 @@ struct Workspace {
   uint32_t units;
   int key_bytes;
 };
+
+// Radix sort shape for keys of `bits` significant bits.
+struct RadixPlan {
+  int digit_bits;
+  int passes;
+};
+RadixPlan radix_plan(int bits, int key_bytes);
+
+// Bytes to clear before a call whose sort follows `plan`.
+size_t zero_bytes_for(const Workspace &w, const RadixPlan &plan);
 
 // Computes the layout; with base == nullptr only sizes are filled in.
 Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool need_grad_row,

@@ -88,3 +88,21 @@ def test_device_input_and_key_bound(gpu_device, no_device_errors):
         np.testing.assert_array_equal(inverse.cpu().numpy(), ei)
         np.testing.assert_array_equal(first.cpu().numpy(), ef)
     no_device_errors()
+
+
+@pytest.mark.parametrize("bits", [9, 10, 16, 17, 18, 19, 20, 24, 25, 26, 27, 28, 30, 32, 36])
+def test_every_radix_plan(gpu_device, no_device_errors, bits):
+    """Key widths that select each digit width (8, 9, 10 bits) and pass count, 32- and 64-bit keys."""
+    from flare_amd.unique import unique_first_occurrence
+
+    rng = np.random.default_rng(bits)
+    n = 70000
+    values = rng.integers(0, 1 << bits, n, dtype=np.uint64).astype(np.int64)
+    values[rng.random(n) < 0.3] = 0  # a hot key at the bottom of the range
+    values[0], values[1] = 0, (1 << bits) - 1  # span exactly `bits` bits
+    unique, inverse, first = unique_first_occurrence(values)
+    eu, ei, ef = O.unique_first_occurrence_sorted(values)
+    np.testing.assert_array_equal(unique, eu)
+    np.testing.assert_array_equal(inverse, ei)
+    np.testing.assert_array_equal(first, ef)
+    no_device_errors()

@@ -184,3 +184,32 @@ def test_csr_ragged_bags_bit_exact(gpu_device, no_device_errors, storage, poolin
     np.testing.assert_array_equal(first.cpu().numpy(), ef)
     np.testing.assert_array_equal(g.cpu().numpy(), eg)
     no_device_errors()
+
+
+def test_shard_with_25_bit_rows(gpu_device, no_device_errors):
+    """Tables totalling 2^25 rows: 25-bit row keys (three 9-bit radix passes) on the CSR path."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    rng = np.random.default_rng(25)
+    table_rows = [1 << 24, (1 << 24) - 1000, 1000]
+    batch, dim = 4096, 4
+    lengths = rng.integers(0, 4, size=len(table_rows) * batch)
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    ids = (rng.integers(0, 1 << 40, size=int(offsets[-1])) % np.asarray(table_rows)[bag_table]).astype(np.int64)
+    ids[rng.random(ids.size) < 0.2] = 0  # hot first rows
+    shard = PooledTableShard(table_rows, dim, value_dtype="float32", initializer=Uniform(-1.0, 1.0), seed=3)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    pooled = shard.lookup_pooled(ids, offsets, batch)
+    grad = rng.normal(0, 1, size=(batch, len(table_rows), dim)).astype(np.float32)
+    unique, inverse, first, g = shard.reduce_pooled_gradients(ids, offsets, batch, grad)
+    shard.synchronize()
+    expected = O.gather_pooled_csr(shard.table.cpu().numpy(), ids, offsets, row_base, batch, dim)
+    np.testing.assert_array_equal(pooled.cpu().numpy(), expected)
+    eu, ei, ef, eg = O.pooled_grad_sums(ids, offsets, row_base, batch, dim, grad)
+    np.testing.assert_array_equal(unique.cpu().numpy(), eu)
+    np.testing.assert_array_equal(inverse.cpu().numpy(), ei)
+    np.testing.assert_array_equal(first.cpu().numpy(), ef)
+    np.testing.assert_array_equal(g.cpu().numpy(), eg)
+    no_device_errors()
