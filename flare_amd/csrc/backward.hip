@@ -213,9 +213,9 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
 // pooling, the bag length of every occurrence.
 constexpr int kPrepMaxBags = 4096;
 
-// Bags per prepare block: about 2048 blocks, at most kPrepMaxBags bags each.
+// Bags per prepare block: about 512 blocks (fewer histogram flushes), at most kPrepMaxBags bags each.
 int prep_bags_per_block(int64_t bags) {
-  return static_cast<int>(std::min<int64_t>(kPrepMaxBags, std::max<int64_t>(64, ceil_div(bags, 2048))));
+  return static_cast<int>(std::min<int64_t>(kPrepMaxBags, std::max<int64_t>(64, ceil_div(bags, 512))));
 }
 
 template <typename IdT>
@@ -887,7 +887,7 @@ __device__ __forceinline__ float scaled(const UpdateArgs &a, float x, float sc) 
 
 // Segment sums of the long keys.  One group of G lanes per unit of
 // kReduceUnit sorted positions lists the unit's positions that belong to long
-// keys and streams their gradient rows four at a time, in order; at each key
+// keys and streams their gradient rows eight at a time, in order; at each key
 // head the running fp32 sum of the finished piece is stored and restarted.  A
 // piece holding a whole key goes to its destination (the per-key sums for an
 // optimizer, or straight to the output for scatter / reduced gradients); a
@@ -1028,12 +1028,12 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
     }
   };
 
-  for (int i0 = 0; i0 < nlong; i0 += 4) {
-    float x[4][NC][VEC];
-    float sc[4];
-    int pos[4];
+  for (int i0 = 0; i0 < nlong; i0 += 8) {
+    float x[8][NC][VEC];
+    float sc[8];
+    int pos[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 8; ++t) {
       const bool ok = i0 + t < nlong;
       pos[t] = ok ? s_list[group][i0 + t] : 0;
       const int64_t gr = ok ? static_cast<int64_t>(s_grow[group][pos[t]]) : 0;
@@ -1050,7 +1050,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
       }
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 8; ++t) {
       if (i0 + t >= nlong) break;
       const int p = pos[t];
       if (piece_first >= 0 && ((heads >> p) & 1ull)) {
@@ -1302,10 +1302,7 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
   return FLARE_OK;
 }
 
-// apply_kernel runs half-width lane groups (twice the columns per lane) where
-// the row allows, so that twice as many keys are in flight per wave.
-constexpr int kApplyG(int g, int nc) { return (g > 8 && nc == 1) ? g / 2 : g; }
-constexpr int kApplyNC(int g, int nc) { return (g > 8 && nc == 1) ? 2 : nc; }
+
 
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
@@ -1327,8 +1324,7 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
 #define FLARE_UPDATE_PAIR(G_, NC_)                                             \
   sums_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);            \
   fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
-  apply_kernel<Tag, VEC, kApplyG(G_, NC_), kApplyNC(G_, NC_), MODE>                 \
-      <<<apply_grid(kApplyG(G_, NC_)), 256, 0, s>>>(a);
+  apply_kernel<Tag, VEC, G_, NC_, MODE><<<apply_grid(G_), 256, 0, s>>>(a);
   if (sh.nc == 1) {
     switch (sh.g) {
       case 8: FLARE_UPDATE_PAIR(8, 1) break;

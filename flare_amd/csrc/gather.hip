@@ -67,7 +67,10 @@ struct PooledArgs {
   int *err;
 };
 
-constexpr int kBagsPerGroup = 8;
+// Bags per lane group: 4 when the block stages its rows in LDS (32 KiB for
+// 128 bf16 rows of 128), 8 when rows are stored directly.
+constexpr int kBagsPerGroupStaged = 4;
+constexpr int kBagsPerGroupDirect = 8;
 
 // Resolve one id to a table row (or -1 for a pad / out-of-range slot).
 template <bool kCsr, typename IdT>
@@ -93,10 +96,16 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // (G ids per lane-parallel load, each lane finding its bag from the running
 // lengths), gathers rows kDepth at a time regardless of bag boundaries
 // (packed, so four rows of loads are in flight per lane), accumulates in
-// occurrence order, and stores a bag's pooled row when the stream passes the
+// occurrence order, and emits a bag's pooled row when the stream passes the
 // bag's end.  Lane l holds L vectors of VEC elements at columns (q*G + l)*VEC.
-template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT>
+// kStage: finished rows go to LDS and the block writes its whole range once,
+// after all of its row loads, with coalesced nontemporal 16-byte stores (a
+// wave's loads and stores share one in-order completion counter, so stores
+// issued between loads would lengthen every later wait).  Otherwise each row
+// is stored when finished.
+template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
+  constexpr int kBagsPerGroup = kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect;
   using E = typename Tag::elem;
   using R = RawVec<Tag, VEC>;
   constexpr int kGroups = kThreads / G;
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
 
   const int lb0 = group * kBagsPerGroup;  // first output row of this group, block-local
   const int nb = static_cast<int>(nout - lb0 < kBagsPerGroup ? nout - lb0 : kBagsPerGroup);
-  if (nb <= 0) return;
+  if (!kStage && nb <= 0) return;  // a staging block still joins the final barrier
   // running start of each bag in the group's virtual id sequence
   int64_t pre[kBagsPerGroup + 1];
   pre[0] = 0;
@@ -148,11 +157,13 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
 
   const E *table = static_cast<const E *>(a.table);
   E *out = static_cast<E *>(a.out);
+  extern __shared__ uint4 s_stage[];  // kStage: the block's pooled rows [nout][D]
+  E *staged = reinterpret_cast<E *>(s_stage);
   const int D = a.dim;
   const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
   const bool mean = a.pooling == FLARE_POOL_MEAN;
 
-  for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
+  for (int c0 = 0; nb > 0 && c0 < D; c0 += G * VEC * L) {
     float acc[L][VEC];
 #pragma unroll
     for (int q = 0; q < L; ++q)
@@ -171,7 +182,10 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
           for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
         }
         const int col = c0 + (q * G + lane) * VEC;
-        if (col < D) store_from_f32_stream<Tag, VEC>(out + out_row * D + col, acc[q]);
+        if (col < D) {
+          if constexpr (kStage) store_from_f32<Tag, VEC>(staged + static_cast<int64_t>(lb0 + cur) * D + col, acc[q]);
+          else store_from_f32_stream<Tag, VEC>(out + out_row * D + col, acc[q]);
+        }
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
       }
@@ -233,6 +247,16 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
     }
     while (cur < nb) flush();  // the last bag and any empty bags after it
   }
+  if constexpr (kStage) {
+    // one contiguous, fully coalesced write of the block's rows (rows are a
+    // multiple of 16 bytes and the output is 16-byte aligned when staging)
+    __syncthreads();
+    typedef unsigned int U4 __attribute__((ext_vector_type(4)));
+    const int64_t n16 = nout * D * static_cast<int64_t>(sizeof(E)) / 16;
+    U4 *dst = reinterpret_cast<U4 *>(out + o0 * D);
+    const U4 *src = reinterpret_cast<const U4 *>(s_stage);
+    for (int64_t i = threadIdx.x; i < n16; i += kThreads) __builtin_nontemporal_store(src[i], dst + i);
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -243,19 +267,32 @@ int grid_for(int64_t work, int64_t per_block) {
   return static_cast<int>(g < 1 ? 1 : (g > 0x7fffffff ? 0x7fffffff : g));
 }
 
-template <typename Tag, int VEC, int L, bool kCsr, typename IdT>
-int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
-  const int64_t per_block = (kThreads / G) * kBagsPerGroup;
+// Pooled rows of a block are staged in LDS and written in one coalesced pass
+// when they fit this budget (16-byte vectors only).
+constexpr int64_t kStageBytes = 32768;
+
+template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kStage>
+int launch_pooled_gs(const PooledArgs &a, int G, hipStream_t s) {
+  const int64_t per_block = (kThreads / G) * (kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect);
   const int grid = grid_for(a.bags, per_block);
+  const size_t lds = kStage ? static_cast<size_t>(per_block) * a.dim * sizeof(typename Tag::elem) : 0;
   switch (G) {
-    case 4: pooled_kernel<Tag, VEC, 4, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    case 8: pooled_kernel<Tag, VEC, 8, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    case 16: pooled_kernel<Tag, VEC, 16, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    case 32: pooled_kernel<Tag, VEC, 32, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
-    default: pooled_kernel<Tag, VEC, 64, L, kCsr, IdT><<<grid, kThreads, 0, s>>>(a); break;
+    case 4: pooled_kernel<Tag, VEC, 4, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
+    case 8: pooled_kernel<Tag, VEC, 8, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
+    case 16: pooled_kernel<Tag, VEC, 16, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
+    case 32: pooled_kernel<Tag, VEC, 32, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
+    default: pooled_kernel<Tag, VEC, 64, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
   }
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
+}
+
+template <typename Tag, int VEC, int L, bool kCsr, typename IdT>
+int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
+  const int64_t stage = static_cast<int64_t>(kThreads / G) * kBagsPerGroupStaged * a.dim * sizeof(typename Tag::elem);
+  if (VEC * sizeof(typename Tag::elem) == 16 && stage <= kStageBytes)
+    return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, true>(a, G, s);
+  return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, false>(a, G, s);
 }
 
 int group_size(int vectors, int min_g) {
