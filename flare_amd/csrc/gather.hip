@@ -129,6 +129,9 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
       const int64_t bag = t * a.batch + b;
       int64_t lo = a.offsets[bag];
       int64_t hi = a.offsets[bag + 1];
+      // offsets must start at 0, end at num_ids and never decrease
+      if (lo < 0 || hi > a.num_ids || hi < lo || (bag == 0 && lo != 0) || (bag + 1 == a.bags && hi != a.num_ids))
+        record_error(a.err, kErrIndexOutOfRange);
       lo = lo < 0 ? 0 : (lo > a.num_ids ? a.num_ids : lo);
       hi = hi < lo ? lo : (hi > a.num_ids ? a.num_ids : hi);  // decreasing offsets pool nothing
       s_begin[i] = lo;

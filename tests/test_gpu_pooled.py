@@ -213,3 +213,59 @@ def test_shard_with_25_bit_rows(gpu_device, no_device_errors):
     np.testing.assert_array_equal(first.cpu().numpy(), ef)
     np.testing.assert_array_equal(g.cpu().numpy(), eg)
     no_device_errors()
+
+
+@pytest.mark.parametrize("case", [(2, 2048, 0.001, "sum"), (4, 1024, 0.0005, "mean"), (3, 256, 0.0005, "weighted"),
+                                  (1, 512, 0.01, "sum")])
+def test_plan_forward_dedup_apply(gpu_device, no_device_errors, case):
+    """PooledStepPlan: forward(), dedup(), apply() in turn on one stream, two steps (sum, mean, weighted)."""
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    config, batch, row_scale, pooling = case
+    w = make_workload(config, batch=batch, row_scale=row_scale)
+    shard = _shard(w, "rowwise_adagrad")
+    table0 = _host(shard.table.clone())
+    weights = w.weights if pooling == "weighted" else None
+    if pooling == "weighted" and weights is None:
+        weights = np.random.default_rng(4).uniform(0, 1, w.num_ids).astype(np.float32)
+    plan = shard.plan_step(w.ids, w.offsets, w.batch, pooling=pooling, per_sample_weights=weights)
+    grad = torch.from_numpy(pooled_grad_host(w)).to(gpu_device)
+    state = {"acc": np.zeros(w.total_rows, np.float32)}
+    table = table0
+    for _ in range(2):
+        pooled = plan.forward()
+        plan.dedup()
+        plan.apply(grad)
+        shard.synchronize()
+        e_pooled, table, state, e_unique, e_inverse, e_first = O.pooled_step(
+            table, state, w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad.cpu().numpy(),
+            storage=w.value_dtype, pooling=pooling, weights=weights)
+        np.testing.assert_array_equal(_host(pooled), e_pooled)
+        u = int(plan.unique_count.item())
+        np.testing.assert_array_equal(plan.unique[:u].cpu().numpy(), e_unique)
+        np.testing.assert_array_equal(plan.first_indices[:u].cpu().numpy(), e_first)
+        np.testing.assert_array_equal(plan.inverse[:w.num_ids].cpu().numpy(), e_inverse)
+        assert O.storage_ulp_distance(_host(shard.table), table, w.value_dtype).max() <= 1
+        np.testing.assert_allclose(shard.state.state0.cpu().numpy(), state["acc"], rtol=1e-5, atol=0)
+        table = _host(shard.table)
+        state = {"acc": shard.state.state0.cpu().numpy()}
+    no_device_errors()
+
+
+def test_forward_reports_invalid_offsets(gpu_device, no_device_errors):
+    """Decreasing or out-of-range CSR offsets pool nothing out of range and set the error bit
+    (the reference validates offsets, recipes/recsys/ranking/schema/input.py:96-114)."""
+    from flare_amd.store import PooledTableShard
+
+    shard = PooledTableShard([10, 10], 4, value_dtype="float32")
+    ids = np.asarray([1, 2, 3, 4], np.int64)
+    good = np.asarray([0, 1, 2, 3, 4], np.int64)
+    shard.lookup_pooled(ids, good, 2)
+    no_device_errors(0)
+    for bad in (np.asarray([0, 3, 1, 3, 4], np.int64),    # decreasing
+                np.asarray([0, 1, 2, 3, 9], np.int64),    # past the ids
+                np.asarray([1, 1, 2, 3, 4], np.int64)):   # not starting at 0
+        out = shard.lookup_pooled(ids, bad, 2)
+        shard.synchronize()
+        assert np.isfinite(out.cpu().numpy()).all()
+        no_device_errors(1)
