@@ -872,6 +872,8 @@ constexpr uint32_t kShortRun = 8;
 // unit partials are folded by a whole block (fold_kernel) instead of one
 // lane group of apply_kernel.
 constexpr uint32_t kInlineSpan = 8;
+// Partial rows per lane group and fold round (at most; fewer for wide rows).
+constexpr int kFoldDepth = 16;
 
 __device__ __forceinline__ uint32_t grad_row_of(const UpdateArgs &a, uint32_t o) {
   if (a.grad_mode == kGradRowDiv) return o / a.grad_div;
@@ -1209,7 +1211,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
 }
 
 // Hot keys: one block per key folds the key's unit partials in order.  Each
-// round the block's lane groups load kFoldDepth partial rows each into LDS
+// round the block's lane groups load up to kFoldDepth partial rows each into LDS
 // (all loads in flight together), then group 0 adds them left to right: the
 // first unit's slot 1, then slot 0 of every following unit.  Group 0 then
 // applies the update.
@@ -1239,26 +1241,51 @@ __global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
       for (int v = 0; v < VEC; ++v) g[c][v] = 0.0f;
     if (group == 0) load_ahead<Tag, VEC, G, NC, MODE>(a, r, key, ahead, lane);
     for (uint32_t base = 0; base < count; base += chunk) {
-      for (int t = 0; t < depth; ++t) {
+      // all of this group's rows of the round in flight before any LDS store
+      constexpr int kDepthMax = kFoldDepth / NC;  // the host's depth never exceeds it
+      float y[kDepthMax][NC][VEC];
+#pragma unroll
+      for (int t = 0; t < kDepthMax; ++t) {
         const uint32_t k = base + group * depth + t;
-        if (k >= count) break;
-        const uint32_t x = h + k;
-        const float *src = a.partial + (static_cast<size_t>(x) * 2 + (k == 0 ? 1 : 0)) * D;
-        float *dst = s_rows + static_cast<size_t>(group * depth + t) * D;
+        const bool ok = t < depth && k < count;
+        const float *src = a.partial + (static_cast<size_t>(h + (ok ? k : 0)) * 2 + (k == 0 ? 1 : 0)) * D;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           const int col = (c * G + lane) * VEC;
-          if (col < D) {
-            float y[VEC];
-            load_f32<VEC>(src + col, y);
-            store_f32<VEC>(dst + col, y);
-          }
+          if (ok && col < D) load_f32<VEC>(src + col, y[t][c]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kDepthMax; ++t) {
+        const uint32_t k = base + group * depth + t;
+        const bool ok = t < depth && k < count;
+        float *dst = s_rows + static_cast<size_t>(group * depth + (ok ? t : 0)) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (ok && col < D) store_f32<VEC>(dst + col, y[t][c]);
         }
       }
       __syncthreads();
       if (group == 0) {
         const uint32_t m = min(chunk, count - base);
-        for (uint32_t k = 0; k < m; ++k) {
+        uint32_t k = 0;
+        for (; k + 8 <= m; k += 8) {  // eight LDS rows read ahead of the in-order adds
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (col < D) {
+              float y[8][VEC];
+#pragma unroll
+              for (int t = 0; t < 8; ++t) load_f32<VEC>(s_rows + static_cast<size_t>(k + t) * D + col, y[t]);
+#pragma unroll
+              for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) g[c][v] += y[t][v];
+            }
+          }
+        }
+        for (; k < m; ++k) {
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
             const int col = (c * G + lane) * VEC;
@@ -1312,11 +1339,12 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto apply_grid = [&](int g) {
     return static_cast<int>(std::min<int64_t>(65536, std::max<int64_t>(1, ceil_div(a.n, 256 / g))));
   };
-  // fold: partial rows staged per round, at most 32 KiB of LDS
+  // fold: partial rows staged per round, at most 64 KiB of LDS (128 rows of
+  // 128 floats: most hot keys fold in one or two rounds)
   auto fold_depth = [&](int g) {
     const int groups = 256 / g;
-    int depth = 4;
-    while (depth > 1 && static_cast<int64_t>(groups) * depth * a.dim * 4 > 32768) depth >>= 1;
+    int depth = kFoldDepth / sh.nc;
+    while (depth > 1 && static_cast<int64_t>(groups) * depth * a.dim * 4 > 65536) depth >>= 1;
     return depth;
   };
   auto fold_lds = [&](int g) { return static_cast<size_t>(256 / g) * fold_depth(g) * a.dim * 4; };

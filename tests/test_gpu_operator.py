@@ -196,3 +196,19 @@ def test_gather_out_of_range_ids_are_zero_and_flagged(gpu_device, no_device_erro
     op.stream.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy().reshape(4, 2), [[1, 1], [0, 0], [0, 0], [0, 0]])
     no_device_errors(expected=1)
+
+
+@pytest.mark.parametrize("dim", [128, 512, 1024, 2048])
+def test_scatter_hot_key_across_many_units_bit_exact(gpu_device, no_device_errors, dim):
+    """A key with thousands of occurrences (its unit partials folded by one block) at every row width."""
+    op = _op()
+    rng = np.random.default_rng(dim)
+    rows, slots = 50, 3000
+    inverse = rng.integers(0, rows + 1, slots).astype(np.int32)  # rows == pad
+    inverse[rng.random(slots) < 0.5] = 7                          # hot key: ~1500 occurrences, ~24 units
+    grad = rng.standard_normal((slots, dim)).astype(np.float32)
+    out = op.scatter(rows, dim, torch.from_numpy(inverse).to(gpu_device), rows,
+                     torch.from_numpy(grad).to(gpu_device))
+    op.stream.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), O.scatter(rows, dim, inverse, rows, grad))
+    no_device_errors()
