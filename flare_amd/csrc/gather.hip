@@ -71,6 +71,14 @@ struct PooledArgs {
 // 128 bf16 rows of 128), 8 when rows are stored directly.
 constexpr int kBagsPerGroupStaged = 4;
 constexpr int kBagsPerGroupDirect = 8;
+// Long bags (kLong: at least kLongBagLength ids per bag on average): one bag
+// per lane group and kLongDepth rows in flight, so that the longest bag, not
+// the group's total, sets the chain of row loads.
+constexpr int64_t kLongBagLength = 8;
+constexpr int kLongDepth = 8;
+
+template <bool kStage, bool kLong>
+constexpr int bags_per_group() { return kLong ? 1 : (kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect); }
 
 // Resolve one id to a table row (or -1 for a pad / out-of-range slot).
 template <bool kCsr, typename IdT>
@@ -103,14 +111,14 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // wave's loads and stores share one in-order completion counter, so stores
 // issued between loads would lengthen every later wait).  Otherwise each row
 // is stored when finished.
-template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage>
+template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
-  constexpr int kBagsPerGroup = kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect;
+  constexpr int kBagsPerGroup = bags_per_group<kStage, kLong>();
   using E = typename Tag::elem;
   using R = RawVec<Tag, VEC>;
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
-  constexpr int kDepth = 4;
+  constexpr int kDepth = kLong ? kLongDepth : 4;
   __shared__ int64_t s_begin[kBagsPerBlock];
   __shared__ int64_t s_len[kBagsPerBlock];
   __shared__ int64_t s_lo[kBagsPerBlock];
@@ -274,28 +282,29 @@ int grid_for(int64_t work, int64_t per_block) {
 // when they fit this budget (16-byte vectors only).
 constexpr int64_t kStageBytes = 32768;
 
-template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kStage>
+template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 int launch_pooled_gs(const PooledArgs &a, int G, hipStream_t s) {
-  const int64_t per_block = (kThreads / G) * (kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect);
+  const int64_t per_block = (kThreads / G) * bags_per_group<kStage, kLong>();
   const int grid = grid_for(a.bags, per_block);
   const size_t lds = kStage ? static_cast<size_t>(per_block) * a.dim * sizeof(typename Tag::elem) : 0;
   switch (G) {
-    case 4: pooled_kernel<Tag, VEC, 4, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
-    case 8: pooled_kernel<Tag, VEC, 8, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
-    case 16: pooled_kernel<Tag, VEC, 16, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
-    case 32: pooled_kernel<Tag, VEC, 32, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
-    default: pooled_kernel<Tag, VEC, 64, L, kCsr, IdT, kStage><<<grid, kThreads, lds, s>>>(a); break;
+    case 4: pooled_kernel<Tag, VEC, 4, L, kCsr, IdT, kStage, kLong><<<grid, kThreads, lds, s>>>(a); break;
+    case 8: pooled_kernel<Tag, VEC, 8, L, kCsr, IdT, kStage, kLong><<<grid, kThreads, lds, s>>>(a); break;
+    case 16: pooled_kernel<Tag, VEC, 16, L, kCsr, IdT, kStage, kLong><<<grid, kThreads, lds, s>>>(a); break;
+    case 32: pooled_kernel<Tag, VEC, 32, L, kCsr, IdT, kStage, kLong><<<grid, kThreads, lds, s>>>(a); break;
+    default: pooled_kernel<Tag, VEC, 64, L, kCsr, IdT, kStage, kLong><<<grid, kThreads, lds, s>>>(a); break;
   }
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }
 
-template <typename Tag, int VEC, int L, bool kCsr, typename IdT>
+template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kLong>
 int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
-  const int64_t stage = static_cast<int64_t>(kThreads / G) * kBagsPerGroupStaged * a.dim * sizeof(typename Tag::elem);
+  const int64_t stage = static_cast<int64_t>(kThreads / G) * bags_per_group<true, kLong>() * a.dim *
+                        sizeof(typename Tag::elem);
   if (VEC * sizeof(typename Tag::elem) == 16 && stage <= kStageBytes)
-    return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, true>(a, G, s);
-  return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, false>(a, G, s);
+    return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, true, kLong>(a, G, s);
+  return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, false, kLong>(a, G, s);
 }
 
 int group_size(int vectors, int min_g) {
@@ -308,12 +317,15 @@ template <typename Tag, bool kCsr, typename IdT>
 int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   constexpr int kWide = 16 / sizeof(typename Tag::elem);
   const bool wide = (a.dim % kWide == 0) && aligned(a.table, 16) && aligned(a.out, 16);
+  const int64_t ids = kCsr ? a.num_ids : a.bags * a.max_elements;
   if (wide) {
     const int vectors = a.dim / kWide;  // 16-byte vectors per row
-    if (vectors >= 8) return launch_pooled_g<Tag, kWide, 2, kCsr, IdT>(a, group_size(vectors / 2, 4), s);
-    return launch_pooled_g<Tag, kWide, 1, kCsr, IdT>(a, group_size(vectors, 4), s);
+    if (vectors <= 64 && ids >= kLongBagLength * a.bags)
+      return launch_pooled_g<Tag, kWide, 1, kCsr, IdT, true>(a, group_size(vectors, 4), s);
+    if (vectors >= 8) return launch_pooled_g<Tag, kWide, 2, kCsr, IdT, false>(a, group_size(vectors / 2, 4), s);
+    return launch_pooled_g<Tag, kWide, 1, kCsr, IdT, false>(a, group_size(vectors, 4), s);
   }
-  return launch_pooled_g<Tag, 1, 1, kCsr, IdT>(a, group_size(a.dim, 8), s);
+  return launch_pooled_g<Tag, 1, 1, kCsr, IdT, false>(a, group_size(a.dim, 8), s);
 }
 
 template <bool kCsr, typename IdT>
