@@ -147,6 +147,7 @@ RAGGED = [
     (7, 20, 5),      # dim not a multiple of the 16-byte vector: scalar lanes
     (130, 300, 3),   # fp32 rows of 300 (two vectors per lane)
     (5, 1100, 4),    # several column passes
+    (257, 64, 40),   # long bags over 128+ byte rows: table-major blocks, last XCD's range partly empty
 ]
 
 
