@@ -867,11 +867,14 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, 
 // are at most kShortRun of them: apply_kernel sums its gradient rows itself
 // (all loads in flight at once), so no per-key sum is written for it.  Every
 // other key goes through sums_kernel.
-constexpr uint32_t kShortRun = 8;
+constexpr uint32_t kShortRun = 4;
 // A key whose positions span more than kInlineSpan + 1 units is "hot": its
 // unit partials are folded by a whole block (fold_kernel) instead of one
 // lane group of apply_kernel.
 constexpr uint32_t kInlineSpan = 8;
+// Lane groups launched for apply_kernel at most: fewer, busier blocks beat
+// one block per 8 keys once there are more keys than the GPU holds at once.
+constexpr int64_t kApplyGroups = 131072;
 // Partial rows per lane group and fold round (at most; fewer for wide rows).
 constexpr int kFoldDepth = 16;
 
@@ -1334,10 +1337,11 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
-  // apply: one key per group where possible: the key count is only known on the
-  // device, so the grid covers n keys (capped) and idle groups exit at once
+  // apply: the key count is only known on the device, so the grid covers n
+  // keys, one per lane group, up to kApplyGroups groups (more keys loop; idle
+  // groups exit at once)
   auto apply_grid = [&](int g) {
-    return static_cast<int>(std::min<int64_t>(65536, std::max<int64_t>(1, ceil_div(a.n, 256 / g))));
+    return static_cast<int>(std::max<int64_t>(1, ceil_div(std::min<int64_t>(a.n, kApplyGroups), 256 / g)));
   };
   // fold: partial rows staged per round, at most 64 KiB of LDS (128 rows of
   // 128 floats: most hot keys fold in one or two rounds)
