@@ -332,11 +332,14 @@ __global__ void init_minmax_kernel(unsigned long long *out) {
 // ----------------------------------------------------------------------------
 // onesweep radix pass (stable)
 // ----------------------------------------------------------------------------
-template <typename K, int DIGIT>
+// kCarry: a second 32-bit value (the gradient row of each occurrence) moves
+// with the key, so that the last pass leaves it in sorted order.
+template <typename K, int DIGIT, bool kCarry>
 __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     const K *__restrict__ kin, const uint32_t *__restrict__ vin, K *__restrict__ kout,
-    uint32_t *__restrict__ vout, uint32_t n, int pass, const uint32_t *__restrict__ hist,
-    uint32_t *status, uint32_t *ticket, int *err) {
+    uint32_t *__restrict__ vout, const uint32_t *__restrict__ gin, uint32_t *__restrict__ gout,
+    uint32_t n, int pass, const uint32_t *__restrict__ hist, uint32_t *status, uint32_t *ticket,
+    int *err) {
   constexpr int kWaves = kOneThreads / 64;
   constexpr int kRadix = 1 << DIGIT;
   static_assert(kOneThreads >= kRadix, "one thread per digit");
@@ -348,6 +351,7 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
   __shared__ uint32_t s_scan[2][kWaves];
   __shared__ K s_keys[kOneTile];
   __shared__ uint32_t s_vals[kOneTile];
+  __shared__ uint32_t s_gvals[kCarry ? kOneTile : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -360,6 +364,7 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
 
   K key[kOneItems];
   uint32_t val[kOneItems];
+  uint32_t gval[kCarry ? kOneItems : 1];
   uint32_t rank[kOneItems];
 #pragma unroll
   for (int k = 0; k < kOneItems; ++k) {
@@ -367,9 +372,11 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     if (e < n) {
       key[k] = kin[e];
       val[k] = vin ? vin[e] : e;
+      if constexpr (kCarry) gval[k] = gin[e];
     } else {
       key[k] = 0;
       val[k] = 0;
+      if constexpr (kCarry) gval[k] = 0;
     }
   }
   // Stable rank inside the tile: for every item the lanes holding the same
@@ -427,6 +434,7 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
       const uint32_t pos = s_tile_start[dk] + s_wcnt[wave][dk] + rank[k];
       s_keys[pos] = key[k];
       s_vals[pos] = val[k];
+      if constexpr (kCarry) s_gvals[pos] = gval[k];
     }
   }
   __syncthreads();
@@ -438,6 +446,7 @@ __global__ __launch_bounds__(kOneThreads) void onesweep_kernel(
     if (out < n) {  // always true unless a spin guard tripped
       kout[out] = kk;
       vout[out] = s_vals[p];
+      if constexpr (kCarry) gout[out] = s_gvals[p];
     }
   }
 }
@@ -562,7 +571,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     uint32_t *__restrict__ head_bits, uint32_t *__restrict__ head_run,
     uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix,
     uint32_t *__restrict__ run_key,
-    const uint32_t *__restrict__ grad_row, const float *__restrict__ scale,
+    const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
     uint32_t *__restrict__ sorted_grad_row, float *__restrict__ sorted_scale,
     uint32_t *__restrict__ run_grad_row, float *__restrict__ run_scale) {
   __shared__ uint32_t s_cnt[160];
@@ -612,10 +621,15 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
         head_run[o] = r;
       }
       // per sorted position: the gradient row and scale of its occurrence
+      // (grad_sorted: the sort has already put the rows in sorted order)
       if (sorted_grad_row) {
-        const uint32_t gr = grad_row[o];
-        sorted_grad_row[j] = gr;
-        if (head[k]) run_grad_row[r] = gr;
+        if (grad_sorted) {
+          if (head[k]) run_grad_row[r] = sorted_grad_row[j];
+        } else {
+          const uint32_t gr = grad_row[o];
+          sorted_grad_row[j] = gr;
+          if (head[k]) run_grad_row[r] = gr;
+        }
       }
       if (sorted_scale) {
         const float sc = scale[o];
@@ -1404,15 +1418,18 @@ int launch_update(int mode, int dtype, const UpdateArgs &a, const Shape &sh, hip
 }
 
 // Sort keys[0]/implicit iota by the low `bits` bits; returns the buffer index
-// holding the result (0 or 1).
-template <typename K, int DIGIT>
+// holding the result (0 or 1).  kCarry: w.grad_row moves with the keys and
+// ends, sorted, in w.sorted_grad_row (the passes alternate between the two
+// buffers, so the pass count must be odd).
+template <typename K, int DIGIT, bool kCarry>
 int run_passes(const Workspace &w, int passes, int *err, hipStream_t s, int *result) {
   const uint32_t n = static_cast<uint32_t>(w.n);
   int cur = 0;
+  uint32_t *g[2] = {w.grad_row, w.sorted_grad_row};
   for (int p = 0; p < passes; ++p) {
-    onesweep_kernel<K, DIGIT><<<w.sort_tiles, kOneThreads, 0, s>>>(
+    onesweep_kernel<K, DIGIT, kCarry><<<w.sort_tiles, kOneThreads, 0, s>>>(
         static_cast<const K *>(w.keys[cur]), p == 0 ? nullptr : w.vals[cur],
-        static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], n, p,
+        static_cast<K *>(w.keys[cur ^ 1]), w.vals[cur ^ 1], g[p & 1], g[(p & 1) ^ 1], n, p,
         w.hist, w.sort_status + (static_cast<size_t>(p) * w.sort_tiles << DIGIT),
         w.tickets + p, err);
     FLARE_TRY_HIP(hipGetLastError());
@@ -1422,13 +1439,25 @@ int run_passes(const Workspace &w, int passes, int *err, hipStream_t s, int *res
   return FLARE_OK;
 }
 
+// Whether a sort by this plan carries the gradient rows (32-bit keys, digits
+// of at most 9 bits so that the third staging array fits in LDS, and an odd
+// pass count so that the rows end in w.sorted_grad_row).
+bool carries_grad_rows(const Workspace &w, const RadixPlan &plan, int key_bytes) {
+  return key_bytes == 4 && w.grad_row && w.sorted_grad_row && plan.digit_bits <= 9 && (plan.passes & 1);
+}
+
 template <typename K>
-int run_sort(const Workspace &w, const RadixPlan &plan, int *err, hipStream_t s, int *result) {
+int run_sort(const Workspace &w, const RadixPlan &plan, int *err, hipStream_t s, int *result,
+             bool carry = false) {
   if constexpr (sizeof(K) == 4) {
-    if (plan.digit_bits == 9) return run_passes<K, 9>(w, plan.passes, err, s, result);
-    if (plan.digit_bits == 10) return run_passes<K, 10>(w, plan.passes, err, s, result);
+    if (carry) {
+      if (plan.digit_bits == 9) return run_passes<K, 9, true>(w, plan.passes, err, s, result);
+      return run_passes<K, 8, true>(w, plan.passes, err, s, result);
+    }
+    if (plan.digit_bits == 9) return run_passes<K, 9, false>(w, plan.passes, err, s, result);
+    if (plan.digit_bits == 10) return run_passes<K, 10, false>(w, plan.passes, err, s, result);
   }
-  return run_passes<K, 8>(w, plan.passes, err, s, result);
+  return run_passes<K, 8, false>(w, plan.passes, err, s, result);
 }
 
 
@@ -1439,6 +1468,7 @@ int run_sort(const Workspace &w, const RadixPlan &plan, int *err, hipStream_t s,
 struct RunsOutputs {
   uint32_t *run_key;              // or null
   const uint32_t *grad_row;       // gathered into sorted order when non-null
+  int grad_sorted;                // 1: the sort carried the rows into sorted order
   const float *scale;             // gathered into sorted order when non-null
   int64_t *first_indices;         // or null
   void *unique_out;               // or null
@@ -1457,7 +1487,7 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
   scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
   runs_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
       sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_bits, w.head_run,
-      w.meta, head_prefix, o.run_key, o.grad_row, o.scale,
+      w.meta, head_prefix, o.run_key, o.grad_row, o.grad_sorted, o.scale,
       o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
       w.run_grad_row, w.run_scale);
   first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_bits, n, first_prefix);
@@ -1476,10 +1506,11 @@ int dedup_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int
                int *sorted, int64_t *first_indices, void *unique_out, int unique_source,
                const void *values, int value_bytes, int64_t *unique_count,
                const float *scale_src) {
-  FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, sorted));
+  const bool carry = carries_grad_rows(w, plan, 4);
+  FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, sorted, carry));
   const uint32_t n = static_cast<uint32_t>(w.n);
   const uint32_t *sk = static_cast<const uint32_t *>(w.keys[*sorted]);
-  RunsOutputs o{w.run_key, w.grad_row, scale_src, first_indices, unique_out, unique_source,
+  RunsOutputs o{w.run_key, w.grad_row, carry ? 1 : 0, scale_src, first_indices, unique_out, unique_source,
                 values, value_bytes, unique_count};
   return runs_and_rank<uint32_t>(w, sk, w.vals[*sorted], n, sentinel, 1, o, s);
 }
@@ -1680,7 +1711,7 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     FLARE_TRY_HIP(hipGetLastError());
     int sorted = 0;
     FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, &sorted));
-    RunsOutputs o{w.run_key, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+    RunsOutputs o{w.run_key, nullptr, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                   values, value_bytes, unique_count};
     FLARE_TRY(runs_and_rank<uint32_t>(w, static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted],
                                       static_cast<uint32_t>(n), 0u, 0, o, s));
@@ -1699,7 +1730,7 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   FLARE_TRY(run_sort<uint64_t>(w, plan, err, s, &sorted));
-  RunsOutputs o{nullptr, nullptr, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+  RunsOutputs o{nullptr, nullptr, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                 values, value_bytes, unique_count};
   FLARE_TRY(runs_and_rank<uint64_t>(w, static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted],
                                     static_cast<uint32_t>(n), 0ull, 0, o, s));
