@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
-    float *__restrict__ aux, uint32_t *__restrict__ hist, int *err) {
+    float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int *err) {
   __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
@@ -232,13 +232,19 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
   for (int i = threadIdx.x; i <= nb; i += 256) {
     const int64_t o = offsets[bag0 + i];
     s_off[i] = o < 0 ? 0 : (o > n ? n : o);
-    // offsets must start at 0, end at n and never decrease
-    if (o < 0 || o > n || (bag0 + i == 0 && o != 0) || (bag0 + i == bags && o != n))
+    // offsets must start at 0, end at n and never decrease; otherwise some
+    // occurrences belong to no bag (or to two), so the batch is rejected
+    if (o < 0 || o > n || (bag0 + i == 0 && o != 0) || (bag0 + i == bags && o != n)) {
       record_error(err, kErrIndexOutOfRange);
+      *reject = 1;
+    }
   }
   __syncthreads();
   for (int i = threadIdx.x; i < nb; i += 256)
-    if (s_off[i + 1] < s_off[i]) record_error(err, kErrIndexOutOfRange);
+    if (s_off[i + 1] < s_off[i]) {
+      record_error(err, kErrIndexOutOfRange);
+      *reject = 1;
+    }
   const int64_t first = s_off[0];
   const int64_t last = s_off[nb];
   const uint32_t sentinel = static_cast<uint32_t>(key_limit);
@@ -509,7 +515,7 @@ __global__ __launch_bounds__(kSortThreads) void head_count_kernel(const K *__res
     const uint32_t j = base + k * kSortThreads + threadIdx.x;
     if (j < n) {
       const K key = sk[j];
-      const bool valid = !(use_sentinel && key == sentinel);
+      const bool valid = !(use_sentinel && key >= sentinel);
       c += (valid && (j == 0 || sk[j - 1] != key)) ? 1u : 0u;
     }
   }
@@ -573,11 +579,19 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     uint32_t *__restrict__ run_key,
     const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
     uint32_t *__restrict__ sorted_grad_row, float *__restrict__ sorted_scale,
-    uint32_t *__restrict__ run_grad_row, float *__restrict__ run_scale) {
+    uint32_t *__restrict__ run_grad_row, float *__restrict__ run_scale, const uint32_t *reject) {
   __shared__ uint32_t s_cnt[160];
   const int tid = threadIdx.x;
   const uint32_t tile = blockIdx.x;
   const uint32_t base = tile * kSortTile;
+  if (*reject) {  // a rejected batch has no runs: everything after the sort does nothing
+    if (tile == 0 && tid == 0) {
+      meta[0] = 0;
+      meta[1] = 0;
+      run_start[0] = 0;
+    }
+    return;
+  }
   bool valid[kSortItems], head[kSortItems];
   K key[kSortItems];
 #pragma unroll
@@ -587,7 +601,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     head[k] = false;
     if (j < n) {
       key[k] = sk[j];
-      valid[k] = !(use_sentinel && key[k] == sentinel);
+      valid[k] = !(use_sentinel && key[k] >= sentinel);
       head[k] = valid[k] && (j == 0 || sk[j - 1] != key[k]);
     }
   }
@@ -637,7 +651,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
         if (head[k]) run_scale[r] = sc;
       }
     }
-    const bool last = (j + 1 == n) || (use_sentinel && sk[j + 1] == sentinel);
+    const bool last = (j + 1 == n) || (use_sentinel && sk[j + 1] >= sentinel);
     if (last) {
       meta[0] = j + 1;
       meta[1] = r + 1;
@@ -728,6 +742,7 @@ struct UpdateArgs {
   const uint32_t *run_rank;
   int32_t *inverse_out;
   const float *grad;
+  uint32_t grad_rows;  // rows of grad when > 0: gradient rows read from the workspace are checked
   int grad_mode;
   uint32_t grad_div;
   const uint32_t *grad_row;
@@ -892,6 +907,15 @@ constexpr int64_t kApplyGroups = 131072;
 // Partial rows per lane group and fold round (at most; fewer for wide rows).
 constexpr int kFoldDepth = 16;
 
+// Gradient rows recorded in the workspace are in range whenever the batch's
+// offsets were valid; after invalid offsets (reported by the dedup) a row is
+// checked before it is read.
+__device__ __forceinline__ uint32_t checked_grad_row(const UpdateArgs &a, uint32_t gr) {
+  if (a.grad_rows == 0 || gr < a.grad_rows) return gr;
+  record_error(a.err, kErrIndexOutOfRange);
+  return 0;
+}
+
 __device__ __forceinline__ uint32_t grad_row_of(const UpdateArgs &a, uint32_t o) {
   if (a.grad_mode == kGradRowDiv) return o / a.grad_div;
   if (a.grad_mode == kGradRowArray) return a.grad_row[o];
@@ -977,7 +1001,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
       lng = ps < 0 || cross_right || static_cast<uint32_t>(pe - ps) > kShortRun;
       if (lng) {
         const uint32_t j = j0 + p;
-        s_grow[group][p] = a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, occ[q]);
+        s_grow[group][p] = checked_grad_row(a, a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, occ[q]));
         s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f
                             : (a.sorted_scale ? a.sorted_scale[j] : a.scale[occ[q]]);
         if constexpr (MODE == kModeRows) s_dest[group][p] = keyv[q];
@@ -1140,7 +1164,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
       float my_sc = 1.0f;
       if (len == 1 && a.sorted_grad_row && (a.scale_mode == kScaleNone || a.sorted_scale)) {
         // one occurrence: its gradient row was recorded with the key
-        my_gr = a.run_grad_row[r];
+        my_gr = checked_grad_row(a, a.run_grad_row[r]);
         if (a.scale_mode != kScaleNone) my_sc = a.run_scale[r];
       } else if (static_cast<uint32_t>(lane) < len) {
         const uint32_t j = seg_start + lane;
@@ -1153,7 +1177,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
             o = 0;
           }
         }
-        my_gr = a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o);
+        my_gr = checked_grad_row(a, a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o));
         if (a.scale_mode != kScaleNone) my_sc = a.sorted_scale ? a.sorted_scale[j] : a.scale[o];
       }
       for (uint32_t k = 0; k < len; k += 4) {
@@ -1489,7 +1513,7 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
       sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_bits, w.head_run,
       w.meta, head_prefix, o.run_key, o.grad_row, o.grad_sorted, o.scale,
       o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
-      w.run_grad_row, w.run_scale);
+      w.run_grad_row, w.run_scale, w.meta + 3);
   first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_bits, n, first_prefix);
   scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
   rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
@@ -1860,11 +1884,11 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   return dedup_rows(w, plan, sentinel, err, s, &sorted, first_indices_out, unique_out,
@@ -1903,6 +1927,7 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   a.run_rank = w.run_rank;
   a.inverse_out = inverse_out;
   a.grad = pooled_grad;
+  a.grad_rows = static_cast<uint32_t>(batch * num_tables);
   a.grad_mode = kGradRowArray;
   a.grad_row = w.grad_row;
   a.sorted_grad_row = w.sorted_grad_row;

@@ -147,7 +147,7 @@ RAGGED = [
     (7, 20, 5),      # dim not a multiple of the 16-byte vector: scalar lanes
     (130, 300, 3),   # fp32 rows of 300 (two vectors per lane)
     (5, 1100, 4),    # several column passes
-    (257, 64, 40),   # long bags over 128+ byte rows: table-major blocks, last XCD's range partly empty
+    (257, 64, 40),   # long bags (one bag per lane group, 8 rows in flight), partial last block
 ]
 
 
@@ -270,3 +270,34 @@ def test_forward_reports_invalid_offsets(gpu_device, no_device_errors):
         shard.synchronize()
         assert np.isfinite(out.cpu().numpy()).all()
         no_device_errors(1)
+
+
+
+def test_backward_rejects_invalid_offsets(gpu_device, no_device_errors):
+    """A batch whose CSR offsets fail validation updates nothing, reports no unique ids and sets
+    the error bit, after a valid batch has left its sort in the workspace (the reference
+    validates offsets before use, recipes/recsys/ranking/schema/input.py:96-114)."""
+    from flare_amd.store import PooledTableShard
+
+    shard = PooledTableShard([10, 10], 4, value_dtype="float32", seed=3)
+    ids = np.asarray([1, 2, 3, 4], np.int64)
+    good = np.asarray([0, 1, 2, 3, 4], np.int64)
+    grad = np.ones((2, 2, 4), np.float32)
+    shard.apply_pooled_gradients(ids, good, 2, grad)
+    shard.synchronize()
+    no_device_errors(0)
+    table = _host(shard.table.clone())
+    acc = shard.state.state0.cpu().numpy().copy()
+    for bad in (np.asarray([0, 3, 1, 3, 4], np.int64),    # decreasing
+                np.asarray([0, 1, 2, 3, 9], np.int64),    # past the ids
+                np.asarray([1, 1, 2, 3, 4], np.int64)):   # not starting at 0
+        unique, inverse, first = shard.apply_pooled_gradients(ids, bad, 2, grad, return_dedup=True)
+        shard.synchronize()
+        assert unique.numel() == 0 and first.numel() == 0
+        np.testing.assert_array_equal(_host(shard.table), table)
+        np.testing.assert_array_equal(shard.state.state0.cpu().numpy(), acc)
+        no_device_errors(1)
+    shard.apply_pooled_gradients(ids, good, 2, grad)  # the next valid batch is applied
+    shard.synchronize()
+    no_device_errors(0)
+    assert not np.array_equal(_host(shard.table), table)
