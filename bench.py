@@ -88,47 +88,75 @@ def pooled_kernel_traffic(config: int):
     return (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024.0
 
 
-def cpu_baseline(config: int, seconds: float) -> dict:
-    """Time the oracle's C restatement of the reference CPU path on host cores."""
+def _cpu_inputs(w):
+    """Table, optimizer state and pooled gradient of one workload for the CPU restatement."""
     import numpy as np
 
-    from flare_amd.workload import make_workload
     from oracle import cpu_step as C
 
-    w = make_workload(config, batch_index=0)
-    storage = w.value_dtype
-    s = {"float32": 4, "float16": 2, "bfloat16": 2}[storage]
-    table = C.init_table(w.total_rows, w.dim, storage, -w.init_range, w.init_range, 11)
+    table = C.init_table(w.total_rows, w.dim, w.value_dtype, -w.init_range, w.init_range, 11)
     rng = np.random.default_rng(5)
     grad = (rng.standard_normal((w.batch, w.num_tables, w.dim), dtype=np.float32) * np.float32(1e-3))
-    opt = w.optimizer
-    if opt == "adam":
+    if w.optimizer == "adam":
         state = {"m": np.zeros((w.total_rows, w.dim), np.float32), "v": np.zeros((w.total_rows, w.dim), np.float32),
                  "step": np.zeros(w.total_rows, np.int32)}
-    elif opt == "rowwise_adagrad":
+    elif w.optimizer == "rowwise_adagrad":
         state = {"acc": np.zeros(w.total_rows, np.float32)}
     else:
         state = {}
+    return table, state, grad
+
+
+def _cpu_steps(w, inputs, seconds: float, max_steps: int, min_steps: int = 3) -> tuple[float, int]:
+    """Median seconds per step of the oracle's C restatement of the reference CPU path."""
+    from oracle import cpu_step as C
+
+    table, state, grad = inputs
     times = []
     start = C.now()
-    while (C.now() - start < seconds and len(times) < 50) or len(times) < 3:
+    while (C.now() - start < seconds and len(times) < max_steps) or len(times) < min_steps:
         t0 = C.now()
-        C.pooled_forward(table, storage, w.dim, w.ids, w.offsets, w.num_tables, w.batch, w.row_base(),
+        C.pooled_forward(table, w.value_dtype, w.dim, w.ids, w.offsets, w.num_tables, w.batch, w.row_base(),
                          w.pooling, w.weights)
-        C.pooled_backward(table, storage, w.dim, state, opt, w.ids, w.offsets, w.num_tables, w.batch,
-                          w.row_base(), grad, w.pooling, w.weights)
+        C.pooled_backward(table, w.value_dtype, w.dim, state, w.optimizer, w.ids, w.offsets, w.num_tables,
+                          w.batch, w.row_base(), grad, w.pooling, w.weights)
         times.append(C.now() - t0)
-    med = statistics.median(times)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(config: int, seconds: float) -> dict:
+    """Time the oracle's C restatement of the reference CPU path on host cores: the benched
+    workload with every host thread and with one, and workload 1 (the reference's own
+    CPU-sized case) with every thread."""
+    from flare_amd.workload import make_workload
+    from oracle import cpu_step as C
+
+    cores = C.threads()
+    w = make_workload(config, batch_index=0)
+    inputs = _cpu_inputs(w)
+    med, steps = _cpu_steps(w, inputs, seconds, 50)
+    C.set_threads(1)
+    try:
+        med1, steps1 = _cpu_steps(w, inputs, seconds / 4, 3, min_steps=1)
+    finally:
+        C.set_threads(cores)
+    del inputs
+    w1 = make_workload(1, batch_index=0)
+    med_w1, steps_w1 = _cpu_steps(w1, _cpu_inputs(w1), seconds / 8, 200)
     return {
         "value": w.batch * w.num_tables / med,
         "unit": "pooled rows/s",
-        "cores": C.threads(),
+        "cores": cores,
         "kind": "port",
         "sample": f"C/OpenMP restatement of the reference Numba path (pooled gather, serial per-table "
                   f"first-occurrence hash dedup, keyed scatter, optimizer); workload {config} full batch "
-                  f"of {w.batch} x {w.num_tables} bags, median of {len(times)} steps",
+                  f"of {w.batch} x {w.num_tables} bags, median of {steps} steps",
         "ms_per_step": med * 1e3,
-        "storage_bytes": s,
+        "one_thread": {"value": w.batch * w.num_tables / med1, "ms_per_step": med1 * 1e3, "steps": steps1},
+        "workload_1": {"value": w1.batch * w1.num_tables / med_w1, "ms_per_step": med_w1 * 1e3,
+                       "steps": steps_w1, "cores": cores,
+                       "workload": "1 table of 1e6 rows x 64 fp32, batch 4096, bags U[1,20], Zipf 1.05, "
+                                   "row-wise Adagrad"},
     }
 
 

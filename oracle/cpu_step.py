@@ -30,6 +30,7 @@ def library():
         lib = ctypes.CDLL(str(LIB))
         vp, i32, i64, f32, f64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double
         lib.cpu_threads.restype = ctypes.c_int
+        lib.cpu_set_threads.argtypes = [ctypes.c_int]
         lib.cpu_now.restype = f64
         lib.cpu_init_table.argtypes = [vp, ctypes.c_int, i64, f32, f32, ctypes.c_uint64]
         lib.cpu_pooled_forward.argtypes = [vp, ctypes.c_int, i32, vp, vp, i32, i64, vp, i32, vp, vp]
@@ -46,6 +47,11 @@ def _p(a):
 
 def threads() -> int:
     return int(library().cpu_threads())
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of the following calls (the host's count by default)."""
+    library().cpu_set_threads(int(n))
 
 
 def init_table(rows: int, dim: int, storage: str, lo: float, hi: float, seed: int) -> np.ndarray:

@@ -91,6 +91,7 @@ static inline void store_st(void *t, int st, int64_t i, float v) {
 }
 
 int cpu_threads(void) { return omp_get_max_threads(); }
+void cpu_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 /* Deterministic U(lo, hi) init (splitmix64 per element), parallel. */
 void cpu_init_table(void *table, int st, int64_t count, float lo, float hi, uint64_t seed) {
