@@ -36,6 +36,7 @@ int *device_error_word(int *status);
 enum : int {
   kErrIndexOutOfRange = 1,  // an index outside its table was skipped / zeroed
   kErrSpinGuard = 2,        // a bounded spin-wait gave up (results invalid)
+  kErrCapacity = 4,         // a key map or its table is full (keys left without a row)
 };
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }

@@ -154,6 +154,27 @@ class _TableState:
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         return p(self.state0), p(self.state1), p(self.step)
 
+    def grow(self, rows: int) -> None:
+        """Room for ``rows`` rows: existing rows and state are kept, new rows are zero (state
+        at its initial value)."""
+        rows = int(rows)
+        if rows <= self.rows:
+            return
+
+        def bigger(t: torch.Tensor | None, fill: float = 0.0) -> torch.Tensor | None:
+            if t is None:
+                return None
+            out = torch.full((rows,) + tuple(t.shape[1:]), fill, dtype=t.dtype, device=t.device)
+            out[: t.shape[0]].copy_(t)
+            return out
+
+        self.table = bigger(self.table)
+        fill0 = float(getattr(self.optimizer, "initial_accumulator_value", 0.0))
+        self.state0 = bigger(self.state0, fill0 if isinstance(self.optimizer, RowWiseAdagrad) else 0.0)
+        self.state1 = bigger(self.state1)
+        self.step = bigger(self.step)
+        self.rows = rows
+
 
 class _Workspace:
     """Grow-only device scratch owned by one stream."""
@@ -307,6 +328,140 @@ class EmbeddingStore:
 
     def synchronize(self) -> None:
         self.stream.synchronize()
+
+
+# ----------------------------------------------------------------------------
+# DynamicEmbeddingStore: arbitrary int64 keys through an HBM key -> row map
+# ----------------------------------------------------------------------------
+def _map_slots(rows: int) -> int:
+    """Power-of-two slot count keeping the map at most half full."""
+    slots = 64
+    while slots < 2 * int(rows):
+        slots *= 2
+    return slots
+
+
+class _KeyMap:
+    def __init__(self, slots: int, device: torch.device, stream: torch.cuda.Stream):
+        self.slots = int(slots)
+        nbytes = _native.library().flare_keymap_bytes(self.slots)
+        if nbytes == 0:
+            raise ValueError(f"key map of {slots} slots is not supported (at most 2^30)")
+        self.buffer = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _native.call("flare_keymap_init", self.buffer.data_ptr(), self.slots, int(stream.cuda_stream))
+
+    def count(self) -> int:
+        """Keys holding a row (reads the header: synchronizes)."""
+        return int(self.buffer[:4].view(torch.int32).item())
+
+
+class DynamicEmbeddingStore(EmbeddingStore):
+    """``EmbeddingStore`` over arbitrary int64 keys (INT64_MIN excepted).
+
+    One HBM hash map per dim sends keys to rows of that dim's table.
+    ``lookup_or_insert`` gives new keys rows in the order of their first
+    occurrence and initial values ``Uniform(min_val, max_val)`` drawn from a
+    counter-based hash of ``(seed, key, column)``, so a key's initial row does
+    not depend on the batch it first arrives in (the worker's store,
+    ``dynamic_embedding.py:251-302``, draws new rows from
+    ``se.Uniform(-0.01, 0.01)``, ``:262-263``).  Rows are never evicted:
+    ``reserve`` grows the table and the map; a full table sets device error
+    bit 4 and returns zero rows for the keys left out.
+    """
+
+    def __init__(self, capacity: int, dims: Sequence[int], *, value_dtype: str = "float32",
+                 optimizer: Any = None, initializer: Any = None, seed: int = 0,
+                 device: Any = None):
+        init = initializer or Uniform()
+        if isinstance(init, Zeros):
+            self._init_range = (0.0, 0.0)
+        else:
+            self._init_range = (float(init.min_val), float(init.max_val))
+        self._seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        super().__init__(capacity, dims, value_dtype=value_dtype, optimizer=optimizer,
+                         initializer=Zeros(), seed=seed, device=device)
+        with torch.cuda.stream(self.stream):
+            self.maps = {d: _KeyMap(_map_slots(self.capacity), self.device, self.stream) for d in self.tables}
+        self._map_workspace = _Workspace(self.device)
+
+    # -- keys -> rows -----------------------------------------------------------
+    def _resolve(self, keys: torch.Tensor, dim: int, insert: bool, values: bool):
+        table = self._table(dim)
+        kmap = self.maps[int(dim)]
+        n = int(keys.numel())
+        rows = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
+        out = torch.empty((n, table.dim), dtype=table.table.dtype, device=self.device) if values else None
+        if n:
+            nbytes = _native.library().flare_keymap_workspace_bytes(n)
+            ws = self._map_workspace.get(nbytes)
+            lo, hi = self._init_range
+            _native.call(
+                "flare_keymap_lookup_or_insert", kmap.buffer.data_ptr(), kmap.slots, keys.data_ptr(), n,
+                1 if insert else 0, table.table.data_ptr(), storage_code(table.table.dtype), table.rows,
+                table.dim, lo, hi, self._seed, rows.data_ptr(), None if out is None else out.data_ptr(),
+                ws.data_ptr(), nbytes, int(self.stream.cuda_stream),
+            )
+        return rows[:n], out
+
+    def rows(self, keys: Any, dim: int, *, insert: bool = False) -> torch.Tensor:
+        """Row of every key in ``dim``'s table (int32, -1 when absent)."""
+        with torch.cuda.stream(self.stream):
+            return self._resolve(self._keys(keys), dim, insert, values=False)[0]
+
+    def lookup(self, keys: Any, dim: int):
+        """Rows of present keys, zeros for absent ones (``[n, dim]``, value dtype)."""
+        with torch.cuda.stream(self.stream):
+            return self._resolve(self._keys(keys), dim, False, values=True)[1], None
+
+    def lookup_or_insert(self, keys: Any, dim: int):
+        with torch.cuda.stream(self.stream):
+            return self._resolve(self._keys(keys), dim, True, values=True)[1], None
+
+    def contains(self, keys: Any, dim: int | None = None) -> np.ndarray:
+        d = next(iter(self.tables)) if dim is None else int(dim)
+        rows = self.rows(keys, d)
+        self.stream.synchronize()
+        return rows.cpu().numpy() >= 0
+
+    def size(self, dim: int | None = None) -> int:
+        """Keys holding a row in ``dim``'s table (all tables when None); synchronizes."""
+        self.stream.synchronize()
+        if dim is not None:
+            return self.maps[int(dim)].count()
+        return sum(m.count() for m in self.maps.values())
+
+    def total_size(self) -> int:
+        return self.size()
+
+    def reserve(self, capacity: int, dim: int) -> None:
+        table = self._table(dim)
+        capacity = int(capacity)
+        if capacity <= table.rows:
+            return
+        with torch.cuda.stream(self.stream):
+            table.grow(capacity)
+            old = self.maps[int(dim)]
+            slots = _map_slots(capacity)
+            if slots > old.slots:
+                new = _KeyMap(slots, self.device, self.stream)
+                _native.call("flare_keymap_rehash", old.buffer.data_ptr(), old.slots, new.buffer.data_ptr(),
+                             new.slots, int(self.stream.cuda_stream))
+                self.maps[int(dim)] = new
+        self.capacity = max(self.capacity, capacity)
+
+    # -- gradients are kept per row ----------------------------------------------
+    def accumulate_gradients(self, keys: Any, grad: Any) -> None:
+        """Keys must have rows (looked up or inserted before); others set device error bit 1
+        and their gradient is dropped at ``optimizer_step``."""
+        with torch.cuda.stream(self.stream):
+            g = to_device(grad, self.device)
+            if g.dim() != 2:
+                raise ValueError(f"gradient must be [keys, dim], got shape {tuple(g.shape)}")
+            k = self._keys(keys)
+            if g.shape[0] != k.numel():
+                raise ValueError(f"gradient shape {tuple(g.shape)} does not match {k.numel()} keys")
+            rows = self._resolve(k, int(g.shape[1]), False, values=False)[0].to(torch.int64)
+        super().accumulate_gradients(rows, g)
 
 
 # ----------------------------------------------------------------------------

@@ -240,9 +240,54 @@ int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t d
                        int32_t *inverse_out, void *workspace, size_t workspace_bytes,
                        void *stream);
 
-/* Reads back and clears the device-side error word that kernels set when they
- * meet an out-of-range index (written as 0 / ignored) or an exhausted
- * spin-wait guard.  Synchronizes the stream.  Returns the flag bits. */
+/* ---------------------------------------------------------------------------
+ * Dynamic key -> row map (the dynamic store's lookup_or_insert).
+ *
+ * Replaces the key index of sparse_embedding.EmbeddingStore as
+ * DynamicSparseEmbeddingSPMD drives it: lookup_or_insert(keys, dim)
+ * (src/flare/runtime/fluxway/workers/dynamic_embedding.py:397-399), new rows
+ * drawn from Uniform(min_val, max_val) (:262-263), reserve(capacity, dim)
+ * (:296-302).  Keys are arbitrary int64 except INT64_MIN; rows index a
+ * caller-owned table of row_capacity rows.  Each call gives new keys rows
+ * row_count, row_count+1, ... in the order of their first occurrence in
+ * `keys` and writes their initial values: element (key, c) is
+ * lo + (hi - lo) * u with u = 24 bits of splitmix64 mixing of
+ * (seed, key, c), scaled to [0, 1), rounded to the storage dtype.
+ * Calls on one map must be ordered (one stream).
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of a map with `capacity` slots (a power of two in [64, 2^30]); 0 when
+ * the capacity is invalid.  Keep the load (keys / capacity) at or below 1/2. */
+size_t flare_keymap_bytes(int64_t capacity);
+
+/* Empties a map buffer (no keys, row count 0). */
+int flare_keymap_init(void *map, int64_t capacity, void *stream);
+
+/* Device workspace of one lookup_or_insert call over n keys. */
+size_t flare_keymap_workspace_bytes(int64_t n);
+
+/* rows_out[i] (int32, optional) = row of keys[i]; values_out[i, :] (optional,
+ * storage dtype, [n, dim]) = its values.  insert != 0: missing keys get rows
+ * (see above; table required).  insert == 0: missing keys give row -1 and
+ * zero values.  A full map or table sets device error bit 4 and leaves the
+ * key without a row (-1).  table may be NULL for a row-only lookup. */
+int flare_keymap_lookup_or_insert(void *map, int64_t capacity, const int64_t *keys,
+                                  int64_t n, int32_t insert, void *table,
+                                  int32_t value_dtype, int64_t row_capacity,
+                                  int32_t dim, float init_lo, float init_hi,
+                                  uint64_t seed, int32_t *rows_out,
+                                  void *values_out, void *workspace,
+                                  size_t workspace_bytes, void *stream);
+
+/* Re-inserts every key of src (and the row count) into dst, which it first
+ * empties: growing a map on reserve(). */
+int flare_keymap_rehash(const void *src, int64_t src_capacity, void *dst,
+                        int64_t dst_capacity, void *stream);
+
+/* Reads back and clears the device-side error word that kernels set: bit 1 an
+ * out-of-range index (written as 0 / ignored) or invalid CSR offsets, bit 2 an
+ * exhausted spin-wait guard, bit 4 a full key map or table.  Synchronizes the
+ * stream.  Returns the flag bits. */
 int32_t flare_take_device_errors(void *stream);
 
 #ifdef __cplusplus

@@ -29,6 +29,14 @@ How each part is pinned (tests/test_oracle.py, tests/test_golden.py):
 * rowwise_adagrad_update: the optax closed form it reduces to at D == 1 and
   the row mean of squares.
 * sgd_update: the flush-window known answer.
+* KeyMap (the dynamic store's key -> row map): a dict restatement of
+  first-occurrence row assignment, checked by closed-form sequences and
+  invariants; its mixing function splitmix64 by the published SplitMix64
+  outputs for seed 1234567; keymap_initial_values by its range, moments and
+  independence from the batch.  The initial values themselves have no
+  counterpart in the reference (its store's initializer stream is external):
+  parity unpinned against the reference, pinned only as this build's own
+  definition.
 
 Parity unpinned (only the external sparse_embedding store defines these, and
 it is not available here): the rounding of updated fp16 / bf16 rows (RNE is
@@ -635,3 +643,63 @@ def storage_ulp_distance(a, b, storage: str) -> np.ndarray:
     def key(i):
         return np.where(i & 0x8000, -(i & 0x7FFF), i)
     return np.abs(key(ia) - key(ib))
+
+
+# --------------------------------------------------------------------------
+# dynamic key -> row map (the dynamic store's lookup_or_insert)
+# The reference drives an external store: lookup_or_insert(keys, dim)
+# (dynamic_embedding.py:397-399) with new rows from Uniform(-0.01, 0.01)
+# (:262-263).  This restates this build's definition of it.
+# --------------------------------------------------------------------------
+_MIX1 = np.uint64(0xBF58476D1CE4E5B9)
+_MIX2 = np.uint64(0x94D049BB133111EB)
+_GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+
+
+def splitmix64_mix(z: np.ndarray) -> np.ndarray:
+    """The SplitMix64 output function (Steele, Lea, Flood 2014) on uint64 arrays (wrapping)."""
+    z = np.asarray(z, dtype=np.uint64)
+    z = (z ^ (z >> np.uint64(30))) * _MIX1
+    z = (z ^ (z >> np.uint64(27))) * _MIX2
+    return z ^ (z >> np.uint64(31))
+
+
+def keymap_initial_values(keys, dim: int, lo: float, hi: float, seed: int, storage: str) -> np.ndarray:
+    """Initial row of each key: element c is ``lo + (hi - lo) * u`` (float32 operations) with
+    ``u = (mix(mix(seed ^ key) + golden * (c + 1)) >> 40) * 2^-24``, then RNE to storage."""
+    k = np.ascontiguousarray(keys, dtype=np.int64).view(np.uint64).reshape(-1, 1)
+    cols = np.arange(1, dim + 1, dtype=np.uint64).reshape(1, -1)
+    with np.errstate(over="ignore"):
+        z = splitmix64_mix(splitmix64_mix(np.uint64(seed) ^ k) + _GOLDEN * cols)
+    u = (z >> np.uint64(40)).astype(np.uint32).astype(np.float32) * np.float32(2.0 ** -24)
+    flo, fhi = np.float32(lo), np.float32(hi)
+    values = flo + (fhi - flo) * u
+    return f32_to_storage(values.astype(np.float32), storage)
+
+
+class KeyMap:
+    """Key -> row map: new keys take rows count, count+1, ... in the order of their first
+    occurrence in each call, until ``row_capacity`` rows are given out; keys left without a row
+    are absent (row -1) and may get one in a later call."""
+
+    def __init__(self, row_capacity: int):
+        self.row_capacity = int(row_capacity)
+        self.rows: dict[int, int] = {}
+
+    def lookup_or_insert(self, keys, insert: bool = True):
+        """Returns (rows int32 [-1 when absent], fresh bool: the key had no row before)."""
+        keys = np.asarray(keys, dtype=np.int64).reshape(-1)
+        rows = np.full(keys.size, -1, dtype=np.int32)
+        fresh = np.zeros(keys.size, dtype=bool)
+        before = dict(self.rows)
+        for i, key in enumerate(keys.tolist()):
+            if key == -(2 ** 63):
+                continue  # not storable
+            row = self.rows.get(key)
+            if row is None and insert and len(self.rows) < self.row_capacity:
+                row = len(self.rows)
+                self.rows[key] = row
+            if row is not None:
+                rows[i] = row
+                fresh[i] = key not in before
+        return rows, fresh
