@@ -160,6 +160,86 @@ def cpu_baseline(config: int, seconds: float) -> dict:
     }
 
 
+def keymap_main(args) -> int:
+    """Dynamic store: lookup_or_insert of one step's unique keys into a 128-wide bf16 table.
+
+    Keys are the unique ids of workload 5 batches (1e8-id space, 131072 bags of U[1,64]
+    Zipf(1.05) ids), in first-occurrence order, mixed into arbitrary int64 keys.  The first
+    call inserts every key; the timed calls rotate over the batches once all are inserted.
+    """
+    import numpy as np
+    import torch
+
+    from flare_amd.store import DynamicEmbeddingStore, Sgd
+    from flare_amd.workload import make_workload
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    dim, batches = 128, max(2, min(args.batches, 4))
+    key_sets = []
+    for k in range(batches):
+        ids = make_workload(5, batch_index=k).ids
+        _, first = np.unique(ids, return_index=True)
+        uids = ids[np.sort(first)].astype(np.uint64)
+        with np.errstate(over="ignore"):  # splitmix64 output function: ids -> arbitrary int64 keys
+            z = (uids ^ (uids >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+            z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+            z = z ^ (z >> np.uint64(31))
+        keys = z.view(np.int64)
+        keys = keys[keys != np.iinfo(np.int64).min]
+        key_sets.append(torch.from_numpy(keys.copy()).to(device))
+    total = len(torch.unique(torch.cat(key_sets)))
+    store = DynamicEmbeddingStore(total + 1024, [dim], value_dtype="bfloat16", optimizer=Sgd(), seed=3)
+    stream = store.stream
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    store.lookup_or_insert(key_sets[0], dim)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    insert_ms = ev[0].elapsed_time(ev[1])
+    for ks in key_sets[1:]:
+        store.lookup_or_insert(ks, dim)
+    for i in range(args.warmup):
+        store.lookup_or_insert(key_sets[i % batches], dim)
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    nkeys = []
+    for i in range(args.steps):
+        ks = key_sets[i % batches]
+        nkeys.append(ks.numel())
+        events[i][0].record(stream)
+        store.lookup_or_insert(ks, dim)
+        events[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in events]
+    med = statistics.median(ms)
+    keys_per_call = statistics.median(nkeys)
+    per_key = 8 + 12 + 4 + 2 * dim * 2  # key in, map slot (key + row word), row out, row read + values out
+    gbs = keys_per_call * per_key / (med * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "dynamic store lookup_or_insert keys/s (steady state, keys present)",
+        "value": keys_per_call / (med * 1e-3),
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_call": med,
+        "higher_is_better": True,
+        "dtype": "bf16 rows",
+        "data": "synthetic (workload 5 unique ids per batch, splitmix64-mixed into int64 keys)",
+        "config": {"workload": f"{keys_per_call:.0f} unique int64 keys per call, 128-wide bf16 table of "
+                               f"{store.tables[dim].rows} rows, map of {store.maps[dim].slots} slots",
+                   "batches": batches, "keys_stored": store.size(dim)},
+        "first_insert_ms": insert_ms,
+        "first_insert_keys": int(key_sets[0].numel()),
+        "roofline": {"kernel": "whole call (probe + values kernels)", "bound": "hbm", "achieved": gbs,
+                     "peak": 8000.0, "unit": "GB/s", "frac": gbs / 8000.0, "traffic": None,
+                     "algorithmic_bytes_per_key": per_key},
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,12 +254,17 @@ def main() -> int:
                          "(a kernel of known traffic, to scale FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--overlap", action="store_true",
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
+    ap.add_argument("--keymap", action="store_true",
+                    help="measure the dynamic store's key map (lookup_or_insert) instead of the pooled step")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only (the tables of one worker's shard on one MI355X); "
               f"--gpus {args.gpus} is not supported by this build", file=sys.stderr)
         return 2
+
+    if args.keymap:
+        return keymap_main(args)
 
     import torch
 

@@ -5,10 +5,11 @@
 // batch it arrives in.
 //
 // Map buffer (flare_keymap_bytes): a 256-byte header (word 0: rows handed out
-// so far), then `capacity` uint64 key words, then `capacity` uint32 row words.
-//   key word: kEmptyKey until a key claims the slot; never changes after.
-//   row word: kEmptyRow (no row), kPending | i (claimed in this call by its
-//             lowest occurrence i), or the key's row (< kPending).
+// so far), then `capacity` 16-byte slots {uint64 key, uint32 row, pad}, so a
+// probe reads key and row with one access.
+//   key: kEmptyKey until a key claims the slot; never changes after.
+//   row: kEmptyRow (no row), kPending | i (claimed in this call by its lowest
+//        occurrence i), or the key's row (< kPending).
 // Slots are found by linear probing from splitmix64(key) (the finaliser of
 // Steele, Lea and Flood's SplitMix64) masked to the power-of-two capacity.
 //
@@ -39,15 +40,15 @@ constexpr int64_t kMaxKeys = int64_t{1} << 30;
 
 struct MapView {
   uint32_t *header;
-  unsigned long long *keys;
-  uint32_t *rows;
+  unsigned long long *slots;  // slot h: key at slots[2h], row word in the low half of slots[2h + 1]
   uint64_t mask;
+  __device__ unsigned long long *key(uint64_t h) const { return slots + 2 * h; }
+  __device__ uint32_t *row(uint64_t h) const { return reinterpret_cast<uint32_t *>(slots + 2 * h + 1); }
 };
 
 MapView view(void *map, int64_t capacity) {
   char *b = static_cast<char *>(map);
   return {reinterpret_cast<uint32_t *>(b), reinterpret_cast<unsigned long long *>(b + kHeaderBytes),
-          reinterpret_cast<uint32_t *>(b + kHeaderBytes + static_cast<size_t>(capacity) * 8),
           static_cast<uint64_t>(capacity - 1)};
 }
 
@@ -68,59 +69,94 @@ __device__ __forceinline__ float init_uniform(uint64_t seed, uint64_t key, uint3
 __global__ __launch_bounds__(kThreads) void init_kernel(MapView m, uint64_t capacity) {
   for (uint64_t i = blockIdx.x * static_cast<uint64_t>(kThreads) + threadIdx.x; i < capacity;
        i += static_cast<uint64_t>(gridDim.x) * kThreads) {
-    m.keys[i] = kEmptyKey;
-    m.rows[i] = kEmptyRow;
+    *m.key(i) = kEmptyKey;
+    *m.row(i) = kEmptyRow;
   }
   if (blockIdx.x == 0 && threadIdx.x < kHeaderBytes / 4) m.header[threadIdx.x] = 0;
 }
 
-// slot_of[i]: the slot of keys[i] (| kFresh when the key had no row before
-// this call), or kNoSlot (absent on lookup, invalid key, or the map is full).
+// code[i]: the row of keys[i] when it has one; kFresh | slot when the key had
+// no row before this call (insert); kNoSlot when absent (lookup), invalid or
+// the map is full.
+// Probe from slot h on (linear), claiming an empty slot on insert; returns the
+// code of occurrence i (see probe_kernel).
+template <bool kInsert>
+__device__ uint32_t probe_from(const MapView &m, unsigned long long k, uint64_t h, uint32_t i, int *err) {
+  uint32_t result = kNoSlot;
+  for (uint64_t probe = 0; probe <= m.mask; ++probe, h = (h + 1) & m.mask) {
+    unsigned long long cur = *m.key(h);
+    if (cur == kEmptyKey) {
+      if (!kInsert) break;  // the key would be here: absent
+      // a stale empty read is harmless: the swap then returns the slot's key
+      cur = atomicCAS(m.key(h), kEmptyKey, k);
+      if (cur == kEmptyKey) cur = k;
+    }
+    if (cur == k) {
+      result = static_cast<uint32_t>(h);
+      break;
+    }
+  }
+  if (result == kNoSlot) {
+    if (kInsert) record_error(err, kErrCapacity);
+    return kNoSlot;
+  }
+  const uint32_t row = *m.row(result);
+  if (row < kPending) return row;
+  if (!kInsert) return kNoSlot;
+  atomicMin(m.row(result), kPending | i);  // no row yet: the lowest occurrence claims it
+  return result | kFresh;
+}
+
+// code[i]: the row of keys[i] when it has one; kFresh | slot when the key had
+// no row before this call (insert); kNoSlot when absent (lookup), invalid or
+// the map is full.  Each thread takes kProbeKeys keys and issues their first
+// slot reads (key and row word in one 16-byte load) together; a key not in
+// its home slot continues in probe_from.
+constexpr int kProbeKeys = 4;
+
 template <bool kInsert>
 __global__ __launch_bounds__(kThreads) void probe_kernel(MapView m, const int64_t *__restrict__ keys, uint32_t n,
                                                          uint32_t *__restrict__ slot_of, int *err) {
-  for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-    const unsigned long long k = static_cast<unsigned long long>(keys[i]);
-    uint32_t result = kNoSlot;
-    if (k == kEmptyKey) {
-      record_error(err, kErrIndexOutOfRange);
-      slot_of[i] = kNoSlot;
-      continue;
+  typedef unsigned long long U2 __attribute__((ext_vector_type(2)));
+  const uint32_t stride = gridDim.x * kThreads * kProbeKeys;
+  for (uint32_t base = blockIdx.x * kThreads * kProbeKeys + threadIdx.x; base < n; base += stride) {
+    unsigned long long k[kProbeKeys];
+    uint64_t h[kProbeKeys];
+    U2 slot[kProbeKeys];
+#pragma unroll
+    for (int p = 0; p < kProbeKeys; ++p) {
+      const uint32_t i = base + p * kThreads;
+      k[p] = i < n ? static_cast<unsigned long long>(keys[i]) : kEmptyKey;
+      h[p] = mix64(k[p]) & m.mask;
     }
-    uint64_t h = mix64(k) & m.mask;
-    for (uint64_t probe = 0; probe <= m.mask; ++probe, h = (h + 1) & m.mask) {
-      unsigned long long cur = m.keys[h];
-      if (cur == kEmptyKey) {
-        if (!kInsert) break;  // the key would be here: absent
-        // a stale empty read is harmless: the swap then returns the slot's key
-        cur = atomicCAS(m.keys + h, kEmptyKey, k);
-        if (cur == kEmptyKey) cur = k;
-      }
-      if (cur == k) {
-        result = static_cast<uint32_t>(h);
-        break;
-      }
+#pragma unroll
+    for (int p = 0; p < kProbeKeys; ++p) {
+      slot[p] = U2{kEmptyKey, 0};
+      if (k[p] != kEmptyKey) slot[p] = *reinterpret_cast<const U2 *>(m.key(h[p]));
     }
-    if (result == kNoSlot) {
-      if (kInsert) record_error(err, kErrCapacity);
-      slot_of[i] = kNoSlot;
-      continue;
-    }
-    if (m.rows[result] >= kPending) {  // no row yet
-      if (kInsert) {
-        atomicMin(m.rows + result, kPending | i);
-        result |= kFresh;
+#pragma unroll
+    for (int p = 0; p < kProbeKeys; ++p) {
+      const uint32_t i = base + p * kThreads;
+      if (i >= n) break;
+      uint32_t code;
+      if (k[p] == kEmptyKey) {
+        record_error(err, kErrIndexOutOfRange);
+        code = kNoSlot;
+      } else if (slot[p].x == k[p] && static_cast<uint32_t>(slot[p].y) < kPending) {
+        code = static_cast<uint32_t>(slot[p].y);  // found in its home slot with a row
+      } else if (!kInsert && slot[p].x == kEmptyKey) {
+        code = kNoSlot;  // absent
       } else {
-        result = kNoSlot;
+        code = probe_from<kInsert>(m, k[p], h[p], i, err);
       }
+      slot_of[i] = code;
     }
-    slot_of[i] = result;
   }
 }
 
 // Whether occurrence i claims its key's row in this call.
 __device__ __forceinline__ bool claims(const MapView &m, uint32_t s, uint32_t i) {
-  return s != kNoSlot && (s & kFresh) && m.rows[s & ~kFresh] == (kPending | i);
+  return s != kNoSlot && (s & kFresh) && *m.row(s & ~kFresh) == (kPending | i);
 }
 
 __global__ __launch_bounds__(kThreads) void count_kernel(MapView m, const uint32_t *__restrict__ slot_of, uint32_t n,
@@ -162,6 +198,7 @@ __global__ __launch_bounds__(1024) void scan_kernel(uint32_t *counts, uint32_t t
     const uint32_t first = header[0];
     const uint64_t end = static_cast<uint64_t>(first) + s_carry;
     meta[0] = first;
+    meta[1] = s_carry;
     header[0] = static_cast<uint32_t>(end < row_capacity ? end : row_capacity);
   }
 }
@@ -173,6 +210,8 @@ __global__ __launch_bounds__(kThreads) void assign_kernel(MapView m, const uint3
   __shared__ uint32_t s_scan[4];
   const uint32_t base = blockIdx.x * kTile;
   uint32_t carry = counts[blockIdx.x];
+  const uint32_t next = blockIdx.x + 1 < gridDim.x ? counts[blockIdx.x + 1] : meta[1];
+  if (next == carry) return;  // no key of this tile is new (block-uniform)
   const uint32_t first = meta[0];
   for (int k = 0; k < kItems; ++k) {  // index order: rounds of 256 consecutive occurrences
     const uint32_t i = base + k * kThreads + threadIdx.x;
@@ -183,9 +222,9 @@ __global__ __launch_bounds__(kThreads) void assign_kernel(MapView m, const uint3
     if (owner) {
       const uint64_t row = static_cast<uint64_t>(first) + carry + ex;
       if (row < row_capacity) {
-        m.rows[s & ~kFresh] = static_cast<uint32_t>(row);
+        *m.row(s & ~kFresh) = static_cast<uint32_t>(row);
       } else {
-        m.rows[s & ~kFresh] = kEmptyRow;  // a later call may retry once rows are reserved
+        *m.row(s & ~kFresh) = kEmptyRow;  // a later call may retry once rows are reserved
         record_error(err, kErrCapacity);
       }
     }
@@ -210,10 +249,14 @@ __global__ __launch_bounds__(kThreads) void values_kernel(MapView m, const int64
     int64_t row = -1;
     bool fresh = false;
     if (s != kNoSlot) {
-      const uint32_t w = m.rows[s & ~kFresh];
-      if (w < kPending) {
-        row = w;
-        fresh = (s & kFresh) != 0;
+      if (s & kFresh) {  // new in this call: its row was assigned after the probe
+        const uint32_t w = *m.row(s & ~kFresh);
+        if (w < kPending) {
+          row = w;
+          fresh = true;
+        }
+      } else {
+        row = s;
       }
     }
     if (lane == 0 && rows_out) rows_out[i] = static_cast<int32_t>(row);
@@ -242,15 +285,15 @@ __global__ __launch_bounds__(kThreads) void rehash_kernel(MapView src, uint64_t 
   if (blockIdx.x == 0 && threadIdx.x == 0) dst.header[0] = src.header[0];
   for (uint64_t j = blockIdx.x * static_cast<uint64_t>(kThreads) + threadIdx.x; j < src_capacity;
        j += static_cast<uint64_t>(gridDim.x) * kThreads) {
-    const unsigned long long k = src.keys[j];
-    const uint32_t r = src.rows[j];
+    const unsigned long long k = *src.key(j);
+    const uint32_t r = *src.row(j);
     if (k == kEmptyKey || r >= kPending) continue;
     uint64_t h = mix64(k) & dst.mask;
     bool placed = false;
     for (uint64_t probe = 0; probe <= dst.mask; ++probe, h = (h + 1) & dst.mask) {
-      const unsigned long long cur = atomicCAS(dst.keys + h, kEmptyKey, k);
+      const unsigned long long cur = atomicCAS(dst.key(h), kEmptyKey, k);
       if (cur == kEmptyKey || cur == k) {
-        dst.rows[h] = r;
+        *dst.row(h) = r;
         placed = true;
         break;
       }
@@ -294,8 +337,8 @@ int launch_values(const MapView &m, const int64_t *keys, const uint32_t *slot_of
   using E = typename Tag::elem;
   E *t = static_cast<E *>(table);
   E *v = static_cast<E *>(values_out);
-  constexpr int kVec = 4;  // 16 B of fp32, 8 B of fp16 / bf16 per lane
-  const bool vec = dim % kVec == 0 && aligned(table, kVec * sizeof(E)) && (!values_out || aligned(values_out, kVec * sizeof(E)));
+  constexpr int kVec = 16 / sizeof(E);  // 16-byte vectors per lane
+  const bool vec = dim % kVec == 0 && aligned(table, 16) && (!values_out || aligned(values_out, 16));
   if (vec) {
     const int vectors = dim / kVec;
     if (vectors <= 8)
@@ -318,7 +361,7 @@ using namespace flare;
 
 extern "C" size_t flare_keymap_bytes(int64_t capacity) {
   if (check_capacity(capacity) != FLARE_OK) return 0;
-  return kHeaderBytes + static_cast<size_t>(capacity) * 12;
+  return kHeaderBytes + static_cast<size_t>(capacity) * 16;
 }
 
 extern "C" int flare_keymap_init(void *map, int64_t capacity, void *stream) {
@@ -363,7 +406,7 @@ extern "C" int flare_keymap_lookup_or_insert(void *map, int64_t capacity, const 
   hipStream_t s = as_stream(stream);
   const MapView m = view(map, capacity);
   const uint32_t un = static_cast<uint32_t>(n);
-  const int pgrid = grid_for(un, kThreads);
+  const int pgrid = grid_for(un, kThreads * kProbeKeys);
   if (insert) {
     const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kTile));
     probe_kernel<true><<<pgrid, kThreads, 0, s>>>(m, keys, un, w.slot_of, err);
