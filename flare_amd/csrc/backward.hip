@@ -53,7 +53,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   };
   const size_t o_hist = take(static_cast<size_t>(kHistCopies) * kMaxPasses * kMaxRadix * 4);
   const size_t o_tickets = take(16 * 4);
-  const size_t o_meta = take(4 * 4);
+  const size_t o_meta = take(8 * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
   const size_t o_head_bits = take(static_cast<size_t>(ceil_div(std::max<int64_t>(n, 1), 32)) * 4);
   // per tile: every plan's passes x 2^digit bits (8 x 256 for 64-bit keys, 3 x 1024 at most for 32-bit)
@@ -138,6 +138,80 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4 *p, size_t n16) {
 
 __global__ __launch_bounds__(256) void zero_f32_kernel(float *p, size_t n) {
   for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += gridDim.x * 256ull) p[i] = 0.0f;
+}
+
+// ----------------------------------------------------------------------------
+// finite check of a gradient (or any storage-dtype array)
+// ----------------------------------------------------------------------------
+__global__ void zero_count_kernel(int64_t *count) {
+  if (threadIdx.x == 0) *count = 0;
+}
+
+// A zero count written by a kernel (not a memset node), so that the call
+// can be captured in a graph.
+int launch_zero_count(int64_t *count, hipStream_t s) {
+  zero_count_kernel<<<1, 64, 0, s>>>(count);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+__global__ void clear_flags_kernel(uint32_t *flag, int32_t *flag_out) {
+  if (threadIdx.x == 0) {
+    if (flag) *flag = 0;
+    if (flag_out) *flag_out = 0;
+  }
+}
+
+// Sets *flag / *flag_out to 1 (and error bit kErrNonFinite) when any of the
+// `count` elements is inf or NaN: exponent bits all ones.
+__global__ __launch_bounds__(256) void nonfinite_kernel(const void *values, int elem_bytes, uint32_t exp_mask,
+                                                        uint64_t count, uint32_t *flag, int32_t *flag_out, int *err) {
+  bool bad = false;
+  const uint64_t tid = blockIdx.x * 256ull + threadIdx.x;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256ull;
+  const uint64_t per16 = 16 / elem_bytes;
+  const uint64_t n16 = (reinterpret_cast<uintptr_t>(values) % 16 == 0) ? count / per16 : 0;
+  const uint4 *v16 = static_cast<const uint4 *>(values);
+  for (uint64_t i = tid; i < n16; i += stride) {
+    const uint4 q = v16[i];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (elem_bytes == 4) bad |= (w[k] & exp_mask) == exp_mask;
+      else bad |= ((w[k] & exp_mask) == exp_mask) || (((w[k] >> 16) & exp_mask) == exp_mask);
+    }
+  }
+  for (uint64_t i = n16 * per16 + tid; i < count; i += stride) {
+    const uint32_t x = elem_bytes == 4 ? static_cast<const uint32_t *>(values)[i]
+                                       : static_cast<const uint16_t *>(values)[i];
+    bad |= (x & exp_mask) == exp_mask;
+  }
+  if (__ballot(bad) && (threadIdx.x & 63) == 0) {
+    if (flag) *flag = 1;
+    if (flag_out) *flag_out = 1;
+    record_error(err, kErrNonFinite);
+  }
+}
+
+// Clears the flags, then checks `count` elements of a float32, float16 or
+// bfloat16 array.
+int launch_finite_check(const void *values, int dtype, int64_t count, uint32_t *flag, int32_t *flag_out, int *err,
+                        hipStream_t s) {
+  uint32_t mask = 0;
+  int bytes = 0;
+  switch (dtype) {
+    case FLARE_FLOAT32: mask = 0x7f800000u; bytes = 4; break;
+    case FLARE_FLOAT16: mask = 0x7c00u; bytes = 2; break;
+    case FLARE_BFLOAT16: mask = 0x7f80u; bytes = 2; break;
+    default: return fail(FLARE_ERR_DTYPE, "finite check requires float16, bfloat16 or float32, got dtype code %d", dtype);
+  }
+  clear_flags_kernel<<<1, 64, 0, s>>>(flag, flag_out);
+  if (count > 0) {
+    const int grid = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, ceil_div(count, 256 * 16 / bytes)), 8192));
+    nonfinite_kernel<<<grid, 256, 0, s>>>(values, bytes, mask, static_cast<uint64_t>(count), flag, flag_out, err);
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
 }
 
 int launch_zero(void *p, size_t bytes, hipStream_t s) {
@@ -741,7 +815,9 @@ struct UpdateArgs {
   const uint32_t *meta;
   const uint32_t *run_rank;
   int32_t *inverse_out;
-  const float *grad;
+  const void *grad;
+  int grad_bf16;       // grad holds bfloat16 (the reference's gradient transport dtype), else float32
+  const uint32_t *reject;  // when non-null and set: a non-finite gradient, the update does nothing
   uint32_t grad_rows;  // rows of grad when > 0: gradient rows read from the workspace are checked
   int grad_mode;
   uint32_t grad_div;
@@ -907,6 +983,14 @@ constexpr int64_t kApplyGroups = 131072;
 // Partial rows per lane group and fold round (at most; fewer for wide rows).
 constexpr int kFoldDepth = 16;
 
+// VEC consecutive gradient elements as float32 (a bfloat16 transport gradient
+// widens exactly, so this equals casting first and reducing after).
+template <int VEC, bool kBf16>
+__device__ __forceinline__ void load_grad(const UpdateArgs &a, int64_t offset, float (&out)[VEC]) {
+  if constexpr (kBf16) load_as_f32<TagBF16, VEC>(static_cast<const uint16_t *>(a.grad) + offset, out);
+  else load_f32<VEC>(static_cast<const float *>(a.grad) + offset, out);
+}
+
 // Gradient rows recorded in the workspace are in range whenever the batch's
 // offsets were valid; after invalid offsets (reported by the dedup) a row is
 // checked before it is read.
@@ -937,8 +1021,9 @@ __device__ __forceinline__ float scaled(const UpdateArgs &a, float x, float sc) 
 // piece of a key that spans units goes to this unit's partial slot (1 = the
 // key's first piece, 0 = a later one) for apply_kernel to fold.  The group
 // also writes the inverse (rank of the key) of every position of the unit.
-template <typename Tag, int VEC, int G, int NC, int MODE>
+template <typename Tag, int VEC, int G, int NC, int MODE, bool kBf16Grad>
 __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
+  if (a.reject && *a.reject) return;
   constexpr int kGroups = 256 / G;
   constexpr int kPPL = kReduceUnit / G;  // sorted positions per lane in the prefetch
   constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
@@ -1085,7 +1170,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
         if (ok && col < D) {
-          load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
+          load_grad<VEC, kBf16Grad>(a, gr * D + col, x[t][c]);
         } else {
 #pragma unroll
           for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
@@ -1129,8 +1214,9 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
 // several units is folded from the unit partials left to right: the first
 // unit's slot 1, then slot 0 of each following unit.  The table row (and
 // Adagrad accumulator) is loaded before the gradient.
-template <typename Tag, int VEC, int G, int NC, int MODE>
+template <typename Tag, int VEC, int G, int NC, int MODE, bool kBf16Grad>
 __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
+  if (a.reject && *a.reject) return;
   constexpr int kGroups = 256 / G;
   constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
   static_assert(G >= static_cast<int>(kShortRun), "one lane per position of a short key");
@@ -1193,7 +1279,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
           for (int c = 0; c < NC; ++c) {
             const int col = (c * G + lane) * VEC;
             if (ok && col < D) {
-              load_f32<VEC>(a.grad + gr * D + col, x[t][c]);
+              load_grad<VEC, kBf16Grad>(a, gr * D + col, x[t][c]);
             } else {
 #pragma unroll
               for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
@@ -1258,6 +1344,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
 // applies the update.
 template <typename Tag, int VEC, int G, int NC, int MODE>
 __global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
+  if (a.reject && *a.reject) return;
   constexpr int kGroups = 256 / G;
   extern __shared__ float s_rows[];  // [kGroups * depth][dim]
   const int lane = threadIdx.x % G;
@@ -1391,10 +1478,12 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   };
   auto fold_lds = [&](int g) { return static_cast<size_t>(256 / g) * fold_depth(g) * a.dim * 4; };
   const int fold_grid = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(a.units, kInlineSpan + 1))));
-#define FLARE_UPDATE_PAIR(G_, NC_)                                             \
-  sums_kernel<Tag, VEC, G_, NC_, MODE><<<grid(G_), 256, 0, s>>>(a);            \
+#define FLARE_UPDATE_PAIR(G_, NC_)                                                          \
+  if (a.grad_bf16) sums_kernel<Tag, VEC, G_, NC_, MODE, true><<<grid(G_), 256, 0, s>>>(a);  \
+  else sums_kernel<Tag, VEC, G_, NC_, MODE, false><<<grid(G_), 256, 0, s>>>(a);            \
   fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
-  apply_kernel<Tag, VEC, G_, NC_, MODE><<<apply_grid(G_), 256, 0, s>>>(a);
+  if (a.grad_bf16) apply_kernel<Tag, VEC, G_, NC_, MODE, true><<<apply_grid(G_), 256, 0, s>>>(a); \
+  else apply_kernel<Tag, VEC, G_, NC_, MODE, false><<<apply_grid(G_), 256, 0, s>>>(a);
   if (sh.nc == 1) {
     switch (sh.g) {
       case 8: FLARE_UPDATE_PAIR(8, 1) break;
@@ -1580,9 +1669,10 @@ bool vec4_ok(const void *p) { return aligned(p, 16); }
 
 // Shared tail of the keyed-row entry points (scatter, scatter_pooled, sparse_update).
 int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int *err, hipStream_t s, int mode,
-                int dtype, int dim, const float *grad, int grad_mode, uint32_t grad_div,
+                int dtype, int dim, const void *grad, int grad_mode, uint32_t grad_div,
                 float *out, void *table, float *s0, float *s1, int32_t *step,
-                const flare_optimizer *opt, int32_t norm_steps) {
+                const flare_optimizer *opt, int32_t norm_steps, int grad_dtype = FLARE_FLOAT32,
+                int check_finite = 0, int32_t *nonfinite_out = nullptr) {
   int sorted = 0;
   FLARE_TRY(dedup_rows(w, plan, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
                        0, nullptr, nullptr));
@@ -1594,8 +1684,14 @@ int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, in
   a.meta = w.meta;
   a.run_rank = w.run_rank;
   a.grad = grad;
+  a.grad_bf16 = grad_dtype == FLARE_BFLOAT16;
   a.grad_mode = grad_mode;
   a.grad_div = grad_div;
+  if (check_finite) {
+    FLARE_TRY(launch_finite_check(grad, grad_dtype, w.n * static_cast<int64_t>(dim), w.meta + 4, nonfinite_out,
+                                  err, s));
+    a.reject = w.meta + 4;
+  }
   a.scale_mode = kScaleNone;
   a.use_norm = norm_steps != 1;
   a.norm = static_cast<float>(norm_steps);
@@ -1776,7 +1872,7 @@ extern "C" int flare_unique_first_occurrence(const void *values, int32_t key_dty
   if (n > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many keys (%lld)", static_cast<long long>(n));
   hipStream_t s = as_stream(stream);
   if (n == 0) {
-    if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
+    if (unique_count) FLARE_TRY(launch_zero_count(unique_count, s));
     return FLARE_OK;
   }
   switch (key_dtype) {
@@ -1796,11 +1892,44 @@ extern "C" size_t flare_sparse_update_workspace_bytes(int64_t n, int64_t rows, i
   return layout_workspace(nullptr, n, 4, std::max(dim, 1), false, false, true, true).total_bytes;
 }
 
+namespace flare {
+namespace {
+int check_grad_dtype(int32_t grad_dtype) {
+  if (grad_dtype != FLARE_FLOAT32 && grad_dtype != FLARE_BFLOAT16)
+    return fail(FLARE_ERR_DTYPE, "sparse embedding gradient_transport_dtype must be one of ['bfloat16', 'float32'], "
+                "got dtype code %d", grad_dtype);
+  return FLARE_OK;
+}
+}  // namespace
+}  // namespace flare
+
+extern "C" int flare_check_finite(const void *values, int32_t dtype, int64_t count, int32_t *nonfinite_out,
+                                  void *stream) {
+  if (count < 0) return fail(FLARE_ERR_SHAPE, "negative element count");
+  if (!nonfinite_out) return fail(FLARE_ERR_ARGUMENT, "nonfinite_out is required");
+  if (count > 0 && !values) return fail(FLARE_ERR_ARGUMENT, "values are null");
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  return launch_finite_check(values, dtype, count, nullptr, nonfinite_out, err, as_stream(stream));
+}
+
 extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
                                    float *state0, float *state1, int32_t *step,
                                    const flare_optimizer *optimizer, const int64_t *keys, int64_t n,
                                    const float *grad, int32_t normalization_steps, void *workspace,
                                    size_t workspace_bytes, void *stream) {
+  return flare_sparse_update_ex(table, value_dtype, rows, dim, state0, state1, step, optimizer, keys, n, grad,
+                                FLARE_FLOAT32, 0, nullptr, normalization_steps, workspace, workspace_bytes, stream);
+}
+
+extern "C" int flare_sparse_update_ex(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                      float *state0, float *state1, int32_t *step,
+                                      const flare_optimizer *optimizer, const int64_t *keys, int64_t n,
+                                      const void *grad, int32_t grad_dtype, int32_t check_finite,
+                                      int32_t *nonfinite_out, int32_t normalization_steps, void *workspace,
+                                      size_t workspace_bytes, void *stream) {
+  FLARE_TRY(check_grad_dtype(grad_dtype));
   if (storage_bytes(value_dtype) == 0)
     return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
   if (dim <= 0 || rows < 0 || n < 0) return fail(FLARE_ERR_SHAPE, "invalid sparse update sizes");
@@ -1811,7 +1940,14 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
   FLARE_TRY(optimizer_mode(optimizer, &mode));
   if (mode == kModeUnique) return fail(FLARE_ERR_ARGUMENT, "sparse update requires an optimizer (SGD, Adam or row-wise Adagrad)");
   FLARE_TRY(check_state(mode, state0, state1, step));
-  if (n == 0 || rows == 0) return FLARE_OK;
+  if (n == 0 || rows == 0) {  // nothing to update; a requested check still reports
+    if (!check_finite || !nonfinite_out) return FLARE_OK;
+    int st = FLARE_OK;
+    int *err = device_error_word(&st);
+    if (!err) return st;
+    return launch_finite_check(grad, grad_dtype, n * static_cast<int64_t>(dim), nullptr, nonfinite_out, err,
+                               as_stream(stream));
+  }
   Workspace w = layout_workspace(workspace, n, 4, dim, false, false, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
@@ -1827,7 +1963,8 @@ extern "C" int flare_sparse_update(void *table, int32_t value_dtype, int64_t row
                                                    w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   return reduce_rows(w, plan, sentinel, err, s, mode, value_dtype, dim, grad, kGradRowOcc, 1,
-                     nullptr, table, state0, state1, step, optimizer, normalization_steps);
+                     nullptr, table, state0, state1, step, optimizer, normalization_steps, grad_dtype,
+                     check_finite, nonfinite_out);
 }
 
 // ----------------------------------------------------------------------------
@@ -1867,7 +2004,7 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   hipStream_t s = as_stream(stream);
   const int64_t bags = batch * num_tables;
   if (n == 0 || bags == 0) {
-    if (unique_count) FLARE_TRY_HIP(hipMemsetAsync(unique_count, 0, sizeof(int64_t), s));
+    if (unique_count) FLARE_TRY(launch_zero_count(unique_count, s));
     return FLARE_OK;
   }
   Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true, true);
@@ -1903,6 +2040,21 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
                                   int32_t normalization_steps, float *grad_out,
                                   int32_t *inverse_out, void *workspace, size_t workspace_bytes,
                                   void *stream) {
+  return flare_pooled_apply_ex(table, value_dtype, rows, dim, state0, state1, step, optimizer, n, num_tables,
+                               batch, pooling, weights, pooled_grad, FLARE_FLOAT32, 0, nullptr,
+                               normalization_steps, grad_out, inverse_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int flare_pooled_apply_ex(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                                     float *state0, float *state1, int32_t *step,
+                                     const flare_optimizer *optimizer, int64_t n,
+                                     int32_t num_tables, int64_t batch, int32_t pooling,
+                                     const float *weights, const void *pooled_grad, int32_t grad_dtype,
+                                     int32_t check_finite, int32_t *nonfinite_out,
+                                     int32_t normalization_steps, float *grad_out,
+                                     int32_t *inverse_out, void *workspace, size_t workspace_bytes,
+                                     void *stream) {
+  FLARE_TRY(check_grad_dtype(grad_dtype));
   if (storage_bytes(value_dtype) == 0)
     return fail(FLARE_ERR_DTYPE, "sparse embedding value dtype code %d is not float16, bfloat16 or float32", value_dtype);
   FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, weights, true));
@@ -1911,7 +2063,14 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   FLARE_TRY(optimizer_mode(optimizer, &mode));
   if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
   FLARE_TRY(check_state(mode, state0, state1, step));
-  if (n == 0 || batch * num_tables == 0) return FLARE_OK;
+  if (n == 0 || batch * num_tables == 0) {  // nothing to update; a requested check still reports
+    if (!check_finite || !nonfinite_out) return FLARE_OK;
+    int st = FLARE_OK;
+    int *err = device_error_word(&st);
+    if (!err) return st;
+    return launch_finite_check(pooled_grad, grad_dtype, batch * num_tables * static_cast<int64_t>(dim), nullptr,
+                               nonfinite_out, err, as_stream(stream));
+  }
   Workspace w = layout_workspace(workspace, n, 4, dim, true, true, true, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
   int st = FLARE_OK;
@@ -1927,7 +2086,14 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
   a.run_rank = w.run_rank;
   a.inverse_out = inverse_out;
   a.grad = pooled_grad;
+  a.grad_bf16 = grad_dtype == FLARE_BFLOAT16;
   a.grad_rows = static_cast<uint32_t>(batch * num_tables);
+  hipStream_t s = as_stream(stream);
+  if (check_finite) {
+    FLARE_TRY(launch_finite_check(pooled_grad, grad_dtype, batch * num_tables * static_cast<int64_t>(dim),
+                                  w.meta + 4, nonfinite_out, err, s));
+    a.reject = w.meta + 4;
+  }
   a.grad_mode = kGradRowArray;
   a.grad_row = w.grad_row;
   a.sorted_grad_row = w.sorted_grad_row;
@@ -1957,7 +2123,7 @@ extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows
                   vec4_ok(w.partial);
   Shape sh;
   FLARE_TRY(choose_shape(dim, v4, &sh));
-  return launch_update(mode, value_dtype, a, sh, as_stream(stream));
+  return launch_update(mode, value_dtype, a, sh, s);
 }
 
 extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows, int32_t dim,

@@ -37,6 +37,7 @@ enum : int {
   kErrIndexOutOfRange = 1,  // an index outside its table was skipped / zeroed
   kErrSpinGuard = 2,        // a bounded spin-wait gave up (results invalid)
   kErrCapacity = 4,         // a key map or its table is full (keys left without a row)
+  kErrNonFinite = 8,        // a checked gradient held inf / NaN (its update was skipped)
 };
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }

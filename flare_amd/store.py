@@ -33,6 +33,25 @@ from flare_amd.precision import require_sparse_value_dtype
 
 _POOLING = {"sum": _native.POOL_SUM, "mean": _native.POOL_MEAN, "weighted": _native.POOL_WEIGHTED}
 
+# Gradient transport dtypes read as they are (SPARSE_GRADIENT_TRANSPORT_DTYPES,
+# sparse_precision.py:12-14): bfloat16 widens to float32 on load, exactly.
+_GRAD_TRANSPORT = {torch.float32: _native.FLOAT32, torch.bfloat16: _native.BFLOAT16}
+_NONFINITE_MESSAGE = "non-finite sparse values at sparse_native_gradient"
+
+
+def _transport_grad(g: torch.Tensor) -> torch.Tensor:
+    """float32 and bfloat16 gradients are used as they are; others are cast to float32."""
+    if g.dtype not in _GRAD_TRANSPORT:
+        g = g.to(torch.float32)
+    return contiguous(g)
+
+
+def _raise_if_nonfinite(flag: torch.Tensor, stream: torch.cuda.Stream) -> None:
+    """``require_finite_sparse_values`` (sparse_precision.py:121-148): reads the device flag."""
+    stream.synchronize()
+    if int(flag.item()):
+        raise FloatingPointError(_NONFINITE_MESSAGE)
+
 
 # ----------------------------------------------------------------------------
 # optimizer and initializer configs (se.Adam / se.Sgd / se.Uniform / se.Zeros)
@@ -205,9 +224,12 @@ class EmbeddingStore:
 
     def __init__(self, capacity: int, dims: Sequence[int], *, value_dtype: str = "float32",
                  optimizer: Any = None, initializer: Any = None, seed: int = 0,
-                 device: Any = None):
+                 device: Any = None, validate_values: bool = False):
         if not torch.cuda.is_available():
             raise RuntimeError("EmbeddingStore requires a ROCm GPU")
+        if not isinstance(validate_values, bool):
+            raise TypeError("validate_values must be bool")
+        self.validate_values = validate_values
         _native.library()
         self.device = _device_of(device)
         self.capacity = int(capacity)
@@ -279,17 +301,23 @@ class EmbeddingStore:
 
     # -- update ---------------------------------------------------------------
     def accumulate_gradients(self, keys: Any, grad: Any) -> None:
+        """Keyed gradients in float32 or bfloat16 transport (others are cast to float32).  With
+        ``validate_values`` a non-finite gradient raises ``FloatingPointError`` here, before
+        anything accumulates (synchronizes)."""
         with torch.cuda.stream(self.stream):
             k = self._keys(keys)
-            g = to_device(grad, self.device)
-            if g.dtype != torch.float32:
-                g = g.to(torch.float32)
+            g = _transport_grad(to_device(grad, self.device))
             if g.dim() != 2 or g.shape[0] != k.numel():
                 raise ValueError(
                     f"gradient shape {tuple(g.shape)} does not match {k.numel()} keys"
                 )
             self._table(g.shape[1])
-            self._pending.setdefault(int(g.shape[1]), []).append((k, contiguous(g)))
+            if self.validate_values and g.numel():
+                flag = torch.empty(1, dtype=torch.int32, device=self.device)
+                _native.call("flare_check_finite", g.data_ptr(), _GRAD_TRANSPORT[g.dtype], g.numel(),
+                             flag.data_ptr(), int(self.stream.cuda_stream))
+                _raise_if_nonfinite(flag, self.stream)
+            self._pending.setdefault(int(g.shape[1]), []).append((k, g))
 
     def optimizer_step(self, normalization_steps: int) -> None:
         if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
@@ -298,7 +326,10 @@ class EmbeddingStore:
             for dim, items in self._pending.items():
                 table = self._table(dim)
                 keys = items[0][0] if len(items) == 1 else torch.cat([k for k, _ in items])
-                grad = items[0][1] if len(items) == 1 else torch.cat([g for _, g in items])
+                if all(g.dtype == torch.bfloat16 for _, g in items):
+                    grad = items[0][1] if len(items) == 1 else torch.cat([g for _, g in items])
+                else:  # one dtype per call: mixed windows are widened to float32
+                    grad = items[0][1] if len(items) == 1 else torch.cat([g.to(torch.float32) for _, g in items])
                 n = int(keys.numel())
                 if n == 0:
                     continue
@@ -306,10 +337,10 @@ class EmbeddingStore:
                 ws = self._workspace.get(nbytes)
                 s0, s1, st = table.pointers()
                 _native.call(
-                    "flare_sparse_update", table.table.data_ptr(), storage_code(table.table.dtype),
+                    "flare_sparse_update_ex", table.table.data_ptr(), storage_code(table.table.dtype),
                     table.rows, table.dim, s0, s1, st, ctypes.byref(table.native_optimizer),
-                    keys.data_ptr(), n, grad.data_ptr(), int(normalization_steps), ws.data_ptr(),
-                    nbytes, int(self.stream.cuda_stream),
+                    keys.data_ptr(), n, grad.data_ptr(), _GRAD_TRANSPORT[grad.dtype], 0, None,
+                    int(normalization_steps), ws.data_ptr(), nbytes, int(self.stream.cuda_stream),
                 )
             self._pending.clear()
 
@@ -547,14 +578,14 @@ class PooledTableShard:
         return out
 
     def _backward(self, ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
-                  normalization_steps, optimizer_override, want_dedup):
+                  normalization_steps, optimizer_override, want_dedup, validate_values=False):
         if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
             raise ValueError("normalization_steps must be a positive integer")
         with torch.cuda.stream(self.stream):
             ids_t, off = self._csr(ids, offsets, batch_size)
             n = int(ids_t.numel())
             w = self._weights(pooling, per_sample_weights, n)
-            g = contiguous(to_device(pooled_grad, self.device).to(torch.float32))
+            g = _transport_grad(to_device(pooled_grad, self.device))
             if g.numel() != batch_size * self.num_tables * self.dim:
                 raise ValueError("pooled gradient must be [batch, num_tables, dim]")
             opt = optimizer_override if optimizer_override is not None else self.state.native_optimizer
@@ -571,15 +602,23 @@ class PooledTableShard:
             ws = self._workspace.get(nbytes)
             s0, s1, st = self.state.pointers()
             p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-            _native.call(
-                "flare_pooled_backward", self.state.table.data_ptr(),
-                storage_code(self.state.table.dtype), self.total_rows, self.dim, s0, s1, st,
-                ctypes.byref(opt), ids_t.data_ptr(),
-                _native.INT32 if ids_t.dtype == torch.int32 else _native.INT64, n, off.data_ptr(),
-                self.num_tables, batch_size, self.row_base.data_ptr(), _POOLING[pooling], p(w),
-                g.data_ptr(), int(normalization_steps), p(grad_out), p(unique), p(inverse),
-                p(first), p(count), ws.data_ptr(), nbytes, int(self.stream.cuda_stream),
-            )
+            flag = torch.empty(1, dtype=torch.int32, device=self.device) if validate_values else None
+            stream = int(self.stream.cuda_stream)
+            id_code = _native.INT32 if ids_t.dtype == torch.int32 else _native.INT64
+            if g.dtype == torch.float32 and not validate_values:  # the one-call form
+                _native.call(
+                    "flare_pooled_backward", self.state.table.data_ptr(),
+                    storage_code(self.state.table.dtype), self.total_rows, self.dim, s0, s1, st,
+                    ctypes.byref(opt), ids_t.data_ptr(), id_code, n, off.data_ptr(),
+                    self.num_tables, batch_size, self.row_base.data_ptr(), _POOLING[pooling], p(w),
+                    g.data_ptr(), int(normalization_steps), p(grad_out), p(unique), p(inverse),
+                    p(first), p(count), ws.data_ptr(), nbytes, stream,
+                )
+            else:
+                self._dedup_apply(ids_t, id_code, n, off, batch_size, pooling, w, g, opt, flag,
+                                  normalization_steps, grad_out, unique, inverse, first, count, ws, nbytes)
+        if flag is not None:
+            _raise_if_nonfinite(flag, self.stream)
         if unique is None:
             return None
         self.stream.synchronize()  # the count is read on the host
@@ -589,16 +628,37 @@ class PooledTableShard:
             result = result + (grad_out[:u],)
         return result
 
+    def _dedup_apply(self, ids_t, id_code, n, off, batch_size, pooling, w, g, opt, flag, normalization_steps,
+                     grad_out, unique, inverse, first, count, ws, nbytes):
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        s0, s1, st = self.state.pointers()
+        stream = int(self.stream.cuda_stream)
+        _native.call(
+            "flare_pooled_dedup", ids_t.data_ptr(), id_code, n, off.data_ptr(), self.num_tables, batch_size,
+            self.row_base.data_ptr(), self.total_rows, self.dim, _POOLING[pooling], p(unique), p(first),
+            p(count), ws.data_ptr(), nbytes, stream,
+        )
+        _native.call(
+            "flare_pooled_apply_ex", self.state.table.data_ptr(), storage_code(self.state.table.dtype),
+            self.total_rows, self.dim, s0, s1, st, ctypes.byref(opt), n, self.num_tables, batch_size,
+            _POOLING[pooling], p(w), g.data_ptr(), _GRAD_TRANSPORT[g.dtype], 0 if flag is None else 1, p(flag),
+            int(normalization_steps), p(grad_out), p(inverse), ws.data_ptr(), nbytes, stream,
+        )
+
     def apply_pooled_gradients(self, ids: Any, offsets: Any, batch_size: int, pooled_grad: Any, *,
                                pooling: str = "sum", per_sample_weights: Any = None,
-                               normalization_steps: int = 1, return_dedup: bool = False):
+                               normalization_steps: int = 1, return_dedup: bool = False,
+                               validate_values: bool = False):
         """Backward + update: dedup, deterministic segment sum, optimizer on the rows.
 
-        With ``return_dedup`` also returns ``(unique_rows, inverse, first_indices)``
-        (global rows; synchronizes once to read the unique count).
+        ``pooled_grad`` may be float32 or bfloat16 (the gradient transport dtypes; bfloat16 is
+        widened on load).  With ``validate_values`` an inf / NaN gradient updates nothing and
+        raises ``FloatingPointError`` (synchronizes).  With ``return_dedup`` also returns
+        ``(unique_rows, inverse, first_indices)`` (global rows; synchronizes once to read the
+        unique count).
         """
         return self._backward(ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
-                              normalization_steps, None, return_dedup)
+                              normalization_steps, None, return_dedup, validate_values)
 
     def reduce_pooled_gradients(self, ids: Any, offsets: Any, batch_size: int, pooled_grad: Any, *,
                                 pooling: str = "sum", per_sample_weights: Any = None):
@@ -644,6 +704,7 @@ class PooledStepPlan:
             self.first_indices = torch.empty(m, dtype=torch.int64, device=dev)
             self.inverse = torch.empty(m, dtype=torch.int32, device=dev)
             self.unique_count = torch.zeros(1, dtype=torch.int64, device=dev)
+            self.nonfinite = torch.zeros(1, dtype=torch.int32, device=dev)
             self.workspace_bytes = _native.library().flare_pooled_backward_workspace_bytes(
                 self.n, shard.total_rows, shard.dim)
             self.workspace = torch.empty(max(self.workspace_bytes, 1), dtype=torch.uint8, device=dev)
@@ -698,18 +759,26 @@ class PooledStepPlan:
         )
 
     def apply(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
-              grad_out: torch.Tensor | None = None, optimizer: Any = None) -> None:
+              grad_out: torch.Tensor | None = None, optimizer: Any = None,
+              validate_values: bool = False) -> None:
+        """``pooled_grad``: contiguous float32 or bfloat16 ``[batch, num_tables, dim]`` on the
+        shard's device.  ``validate_values`` checks it first: inf / NaN updates nothing and
+        raises ``FloatingPointError`` (this synchronizes)."""
         s = self.shard
-        if pooled_grad.dtype != torch.float32 or not pooled_grad.is_contiguous() or \
+        if pooled_grad.dtype not in _GRAD_TRANSPORT or not pooled_grad.is_contiguous() or \
                 pooled_grad.numel() != self.batch * s.num_tables * s.dim or pooled_grad.device != s.device:
-            raise ValueError("pooled_grad must be a contiguous float32 [batch, num_tables, dim] device tensor")
+            raise ValueError("pooled_grad must be a contiguous float32 or bfloat16 [batch, num_tables, dim] "
+                             "device tensor")
         opt = s.state.native_optimizer if optimizer is None else optimizer
         s0, s1, st = s.state.pointers()
         _native.call(
-            "flare_pooled_apply", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
+            "flare_pooled_apply_ex", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
             s.total_rows, s.dim, s0, s1, st, ctypes.byref(opt), self.n, s.num_tables, self.batch,
             _POOLING[self.pooling], None if self.weights is None else self.weights.data_ptr(),
-            pooled_grad.data_ptr(), int(normalization_steps),
+            pooled_grad.data_ptr(), _GRAD_TRANSPORT[pooled_grad.dtype], 1 if validate_values else 0,
+            self.nonfinite.data_ptr() if validate_values else None, int(normalization_steps),
             None if grad_out is None else grad_out.data_ptr(), self.inverse.data_ptr(),
             self.workspace.data_ptr(), self.workspace_bytes, self._stream,
         )
+        if validate_values:
+            _raise_if_nonfinite(self.nonfinite, s.stream)

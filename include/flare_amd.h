@@ -190,6 +190,30 @@ int flare_sparse_update(void *table, int32_t value_dtype, int64_t rows,
                         int32_t normalization_steps, void *workspace,
                         size_t workspace_bytes, void *stream);
 
+/* flare_sparse_update with the gradient in its transport dtype, cast on load
+ * instead of in a separate pass (train_worker.py:520-527 and
+ * sparse_precision.py:150-192: prepare_sparse_native_gradient casts bf16 / fp32
+ * transport to the fp32 native gradient).  grad_dtype: FLARE_FLOAT32 or
+ * FLARE_BFLOAT16 (SPARSE_GRADIENT_TRANSPORT_DTYPES, sparse_precision.py:12-14);
+ * a bf16 value widens exactly, so the result equals casting first.
+ * check_finite != 0 (validate_values=True, sparse_precision.py:121-148):
+ * the gradient is checked first; if any element is inf / NaN nothing is
+ * updated, *nonfinite_out (device int32, required then) becomes 1 and device
+ * error bit 8 is set; otherwise *nonfinite_out becomes 0. */
+int flare_sparse_update_ex(void *table, int32_t value_dtype, int64_t rows,
+                           int32_t dim, float *state0, float *state1,
+                           int32_t *step, const flare_optimizer *optimizer,
+                           const int64_t *keys, int64_t n, const void *grad,
+                           int32_t grad_dtype, int32_t check_finite,
+                           int32_t *nonfinite_out, int32_t normalization_steps,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/* require_finite_sparse_values (sparse_precision.py:121-148) on the device:
+ * *nonfinite_out (device int32) = 1 when any of the count float32 / float16 /
+ * bfloat16 elements is inf or NaN, else 0.  Sets device error bit 8 too. */
+int flare_check_finite(const void *values, int32_t dtype, int64_t count,
+                       int32_t *nonfinite_out, void *stream);
+
 size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows,
                                              int32_t dim);
 
@@ -240,6 +264,19 @@ int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t d
                        int32_t *inverse_out, void *workspace, size_t workspace_bytes,
                        void *stream);
 
+/* flare_pooled_apply with the pooled gradient in its transport dtype
+ * (FLARE_FLOAT32 or FLARE_BFLOAT16, cast on load) and an optional finite
+ * check, as flare_sparse_update_ex. */
+int flare_pooled_apply_ex(void *table, int32_t value_dtype, int64_t rows, int32_t dim,
+                          float *state0, float *state1, int32_t *step,
+                          const flare_optimizer *optimizer, int64_t n,
+                          int32_t num_tables, int64_t batch, int32_t pooling,
+                          const float *weights, const void *pooled_grad,
+                          int32_t grad_dtype, int32_t check_finite,
+                          int32_t *nonfinite_out, int32_t normalization_steps,
+                          float *grad_out, int32_t *inverse_out, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Dynamic key -> row map (the dynamic store's lookup_or_insert).
  *
@@ -286,8 +323,8 @@ int flare_keymap_rehash(const void *src, int64_t src_capacity, void *dst,
 
 /* Reads back and clears the device-side error word that kernels set: bit 1 an
  * out-of-range index (written as 0 / ignored) or invalid CSR offsets, bit 2 an
- * exhausted spin-wait guard, bit 4 a full key map or table.  Synchronizes the
- * stream.  Returns the flag bits. */
+ * exhausted spin-wait guard, bit 4 a full key map or table, bit 8 a checked
+ * gradient with inf / NaN.  Synchronizes the stream.  Returns the flag bits. */
 int32_t flare_take_device_errors(void *stream);
 
 #ifdef __cplusplus
