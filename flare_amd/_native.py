@@ -72,6 +72,9 @@ SIGNATURES = {
     "flare_keymap_lookup_or_insert": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _i64, _i32, ctypes.c_float,
                                              ctypes.c_float, ctypes.c_uint64, _vp, _vp, _vp, _sz, _vp]),
     "flare_keymap_rehash": (_i32, [_vp, _i64, _vp, _i64, _vp]),
+    "flare_keymap_export_workspace_bytes": (_sz, [_i64]),
+    "flare_keymap_export": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_copy_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp]),
     "flare_take_device_errors": (_i32, [_vp]),
 }
 

@@ -302,6 +302,70 @@ __global__ __launch_bounds__(kThreads) void rehash_kernel(MapView src, uint64_t 
   }
 }
 
+// Export: the keys that hold rows and their rows, in slot order (count per
+// tile of kTile slots, scan, write).
+__global__ __launch_bounds__(kThreads) void export_count_kernel(MapView m, uint64_t capacity,
+                                                                uint32_t *__restrict__ counts) {
+  __shared__ uint32_t s_sum[kThreads / 64];
+  const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kTile;
+  uint32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const uint64_t j = base + k * kThreads + threadIdx.x;
+    if (j < capacity && *m.key(j) != kEmptyKey && *m.row(j) < kPending) ++c;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+  if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[blockIdx.x] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+}
+
+__global__ __launch_bounds__(1024) void export_scan_kernel(uint32_t *counts, uint32_t tiles, int64_t *total) {
+  __shared__ uint32_t s_scan[16];
+  __shared__ uint32_t s_carry;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (uint32_t b = 0; b < tiles; b += 1024) {
+    const uint32_t t = b + threadIdx.x;
+    const uint32_t v = t < tiles ? counts[t] : 0u;
+    const uint32_t ex = block_exclusive_scan<1024>(v, s_scan);
+    const uint32_t carry = s_carry;
+    if (t < tiles) counts[t] = carry + ex;
+    __syncthreads();
+    if (threadIdx.x == 1023) s_carry = carry + ex + v;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *total = s_carry;
+}
+
+__global__ __launch_bounds__(kThreads) void export_write_kernel(MapView m, uint64_t capacity,
+                                                                const uint32_t *__restrict__ counts,
+                                                                int64_t *__restrict__ keys_out,
+                                                                int32_t *__restrict__ rows_out) {
+  __shared__ uint32_t s_scan[4];
+  const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kTile;
+  uint32_t carry = counts[blockIdx.x];
+  for (int k = 0; k < kItems; ++k) {  // slot order: rounds of 256 consecutive slots
+    const uint64_t j = base + k * kThreads + threadIdx.x;
+    bool has = false;
+    unsigned long long key = 0;
+    uint32_t row = 0;
+    if (j < capacity) {
+      key = *m.key(j);
+      row = *m.row(j);
+      has = key != kEmptyKey && row < kPending;
+    }
+    uint32_t round = 0;
+    const uint32_t ex = block_exclusive_scan_256(has ? 1u : 0u, s_scan, &round);
+    if (has) {
+      keys_out[carry + ex] = static_cast<int64_t>(key);
+      rows_out[carry + ex] = static_cast<int32_t>(row);
+    }
+    carry += round;
+  }
+}
+
 int check_capacity(int64_t capacity) {
   if (capacity < kMinCapacity || capacity > kMaxCapacity || (capacity & (capacity - 1)) != 0)
     return fail(FLARE_ERR_ARGUMENT, "key map capacity must be a power of two in [%lld, %lld], got %lld",
@@ -443,6 +507,30 @@ extern "C" int flare_keymap_rehash(const void *src, int64_t src_capacity, void *
       d, static_cast<uint64_t>(dst_capacity));
   rehash_kernel<<<grid_for(static_cast<uint64_t>(src_capacity), kThreads, 4096), kThreads, 0, s>>>(
       view(const_cast<void *>(src), src_capacity), static_cast<uint64_t>(src_capacity), d, err);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
+extern "C" size_t flare_keymap_export_workspace_bytes(int64_t capacity) {
+  if (check_capacity(capacity) != FLARE_OK) return 0;
+  return static_cast<size_t>(ceil_div(capacity, kTile)) * 4 + 256;
+}
+
+extern "C" int flare_keymap_export(const void *map, int64_t capacity, int64_t *keys_out, int32_t *rows_out,
+                                   int64_t *count_out, void *workspace, size_t workspace_bytes, void *stream) {
+  FLARE_TRY(check_capacity(capacity));
+  if (!map || !keys_out || !rows_out || !count_out) return fail(FLARE_ERR_ARGUMENT, "key map export buffers are null");
+  const size_t need = flare_keymap_export_workspace_bytes(capacity);
+  if (!workspace || workspace_bytes < need)
+    return fail(FLARE_ERR_WORKSPACE, "key map export workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const MapView m = view(const_cast<void *>(map), capacity);
+  const uint32_t tiles = static_cast<uint32_t>(ceil_div(capacity, kTile));
+  uint32_t *counts = static_cast<uint32_t *>(workspace);
+  export_count_kernel<<<tiles, kThreads, 0, s>>>(m, static_cast<uint64_t>(capacity), counts);
+  export_scan_kernel<<<1, 1024, 0, s>>>(counts, tiles, count_out);
+  export_write_kernel<<<tiles, kThreads, 0, s>>>(m, static_cast<uint64_t>(capacity), counts, keys_out, rows_out);
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }

@@ -1,0 +1,86 @@
+// Row copies between device tables: gather (dst_index NULL), scatter
+// (src_index NULL) or both.  Used by the stores' assign and checkpoint
+// page-image export / import; rows move as raw bytes, so every dtype
+// (storage values, fp32 optimizer state, int32 step counters) shares it.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace flare {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename U>
+__global__ __launch_bounds__(kThreads) void copy_rows_kernel(const U *__restrict__ src, int64_t src_rows,
+                                                             U *__restrict__ dst, int64_t dst_rows,
+                                                             int64_t units, const int32_t *__restrict__ src_index,
+                                                             const int32_t *__restrict__ dst_index, int64_t n,
+                                                             int *err) {
+  const int64_t total = n * units;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t i = t / units;
+    const int64_t u = t - i * units;
+    const int64_t s = src_index ? src_index[i] : i;
+    const int64_t d = dst_index ? dst_index[i] : i;
+    if (s < 0 || s >= src_rows || d < 0 || d >= dst_rows) {
+      if (u == 0) record_error(err, kErrIndexOutOfRange);
+      continue;
+    }
+    dst[d * units + u] = src[s * units + u];
+  }
+}
+
+}  // namespace
+}  // namespace flare
+
+using namespace flare;
+
+extern "C" int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_rows, int64_t row_bytes,
+                               const int32_t *src_index, const int32_t *dst_index, int64_t n, void *stream) {
+  if (row_bytes <= 0 || row_bytes % 2 != 0 || src_rows < 0 || dst_rows < 0 || n < 0)
+    return fail(FLARE_ERR_SHAPE, "invalid row copy sizes (row_bytes %lld must be a positive multiple of 2)",
+                static_cast<long long>(row_bytes));
+  if (n == 0) return FLARE_OK;
+  if (!src || !dst) return fail(FLARE_ERR_ARGUMENT, "row copy buffers are null");
+  if (!src_index && n > src_rows) return fail(FLARE_ERR_SHAPE, "more rows than the source holds");
+  if (!dst_index && n > dst_rows) return fail(FLARE_ERR_SHAPE, "more rows than the destination holds");
+  int st = FLARE_OK;
+  int *err = device_error_word(&st);
+  if (!err) return st;
+  hipStream_t s = as_stream(stream);
+  int unit = 2;
+  for (int c : {16, 8, 4}) {
+    if (row_bytes % c == 0 && aligned(src, c) && aligned(dst, c)) {
+      unit = c;
+      break;
+    }
+  }
+  const int64_t units = row_bytes / unit;
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n * units, kThreads), 1 << 16));
+  switch (unit) {
+    case 16:
+      copy_rows_kernel<uint4><<<grid, kThreads, 0, s>>>(static_cast<const uint4 *>(src), src_rows,
+                                                        static_cast<uint4 *>(dst), dst_rows, units, src_index,
+                                                        dst_index, n, err);
+      break;
+    case 8:
+      copy_rows_kernel<uint2><<<grid, kThreads, 0, s>>>(static_cast<const uint2 *>(src), src_rows,
+                                                        static_cast<uint2 *>(dst), dst_rows, units, src_index,
+                                                        dst_index, n, err);
+      break;
+    case 4:
+      copy_rows_kernel<uint32_t><<<grid, kThreads, 0, s>>>(static_cast<const uint32_t *>(src), src_rows,
+                                                           static_cast<uint32_t *>(dst), dst_rows, units,
+                                                           src_index, dst_index, n, err);
+      break;
+    default:
+      copy_rows_kernel<uint16_t><<<grid, kThreads, 0, s>>>(static_cast<const uint16_t *>(src), src_rows,
+                                                           static_cast<uint16_t *>(dst), dst_rows, units,
+                                                           src_index, dst_index, n, err);
+      break;
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}

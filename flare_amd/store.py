@@ -344,6 +344,124 @@ class EmbeddingStore:
                 )
             self._pending.clear()
 
+    # -- checkpoint page images and assign ---------------------------------------
+    # Page images as the reference's store hands them to its checkpoint code
+    # (tests/runtime/test_sparse_storage_limits.py:62-79,
+    # tools/validation/audit_sparse_checkpoint.py:33-70): per page the
+    # embedding dim, keys (uint64 view of int64), values [n * dim], optimizer
+    # states [n * width] (Adam: m then v, 2 * dim; row-wise Adagrad: the
+    # accumulator, 1; SGD: none) and per-key update steps (uint32; counted for
+    # Adam only, 0 otherwise).  bfloat16 values are exported as float32.
+    def optimizer_enabled(self) -> bool:
+        return True
+
+    def table_dims(self) -> list[int]:
+        return list(self.tables)
+
+    def key_dtype(self) -> str:
+        return "int64"
+
+    def num_slots(self) -> int:
+        return len(self.tables)
+
+    def _rows_of(self, keys: torch.Tensor, dim: int, insert: bool) -> torch.Tensor:
+        """Rows of keys (int32): the keys themselves in the dense shard."""
+        table = self._table(dim)
+        return contiguous(torch.clamp(keys, -1, table.rows).to(torch.int32))
+
+    def _copy_rows(self, src: torch.Tensor, dst: torch.Tensor, src_index, dst_index, n: int) -> None:
+        row_bytes = src.element_size() * (src[0].numel() if src.dim() > 1 else 1)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        _native.call("flare_copy_rows", src.data_ptr(), src.shape[0], dst.data_ptr(), dst.shape[0], row_bytes,
+                     p(src_index), p(dst_index), n, int(self.stream.cuda_stream))
+
+    def _page(self, table: _TableState, keys: torch.Tensor, rows: torch.Tensor) -> dict:
+        n = int(rows.numel())
+        dev = self.device
+        values = torch.empty((n, table.dim), dtype=table.table.dtype, device=dev)
+        self._copy_rows(table.table, values, rows, None, n)
+        opt = table.optimizer
+        if isinstance(opt, Adam):
+            state = torch.empty((n, 2 * table.dim), dtype=torch.float32, device=dev)
+            m = torch.empty((n, table.dim), dtype=torch.float32, device=dev)
+            v = torch.empty((n, table.dim), dtype=torch.float32, device=dev)
+            self._copy_rows(table.state0, m, rows, None, n)
+            self._copy_rows(table.state1, v, rows, None, n)
+            state[:, : table.dim] = m
+            state[:, table.dim:] = v
+            steps = torch.empty(n, dtype=torch.int32, device=dev)
+            self._copy_rows(table.step, steps, rows, None, n)
+        elif isinstance(opt, RowWiseAdagrad):
+            state = torch.empty((n, 1), dtype=torch.float32, device=dev)
+            self._copy_rows(table.state0, state, rows, None, n)
+            steps = torch.zeros(n, dtype=torch.int32, device=dev)
+        else:
+            state = torch.empty((n, 0), dtype=torch.float32, device=dev)
+            steps = torch.zeros(n, dtype=torch.int32, device=dev)
+        if values.dtype == torch.bfloat16:
+            values = values.to(torch.float32)
+        self.stream.synchronize()
+        return {
+            "embedding_dim": table.dim,
+            "keys": keys.cpu().numpy().view(np.uint64),
+            "values": values.cpu().numpy().reshape(-1),
+            "optimizer_states": state.cpu().numpy().reshape(-1),
+            "steps": steps.cpu().numpy().view(np.uint32),
+        }
+
+    def _stored(self, dim: int):
+        """(keys int64, rows int32) of every stored key of ``dim``'s table, on the device."""
+        table = self._table(dim)
+        rows = torch.arange(table.rows, dtype=torch.int32, device=self.device)
+        return rows.to(torch.int64), rows
+
+    def export_page_images(self, page_keys: int = 1 << 20) -> list[dict]:
+        pages = []
+        with torch.cuda.stream(self.stream):
+            for dim, table in self.tables.items():
+                keys, rows = self._stored(dim)
+                for lo in range(0, int(keys.numel()), int(page_keys)):
+                    hi = min(lo + int(page_keys), int(keys.numel()))
+                    pages.append(self._page(table, keys[lo:hi], contiguous(rows[lo:hi])))
+        return pages
+
+    def import_page_images(self, pages) -> None:
+        """Writes every page's rows (values, optimizer state, steps) for its keys."""
+        with torch.cuda.stream(self.stream):
+            for page in pages:
+                dim = int(page["embedding_dim"])
+                table = self._table(dim)
+                keys = torch.from_numpy(np.asarray(page["keys"], dtype=np.uint64).view(np.int64).copy()).to(self.device)
+                n = int(keys.numel())
+                if n == 0:
+                    continue
+                rows = self._rows_of(keys, dim, insert=True)
+                values = torch.from_numpy(np.asarray(page["values"]).reshape(n, dim)).to(self.device)
+                self._copy_rows(contiguous(values.to(table.table.dtype)), table.table, None, rows, n)
+                state = np.asarray(page["optimizer_states"], dtype=np.float32).reshape(n, -1)
+                if isinstance(table.optimizer, Adam):
+                    st = torch.from_numpy(state).to(self.device)
+                    self._copy_rows(contiguous(st[:, :dim]), table.state0, None, rows, n)
+                    self._copy_rows(contiguous(st[:, dim:]), table.state1, None, rows, n)
+                    steps = torch.from_numpy(np.asarray(page["steps"], dtype=np.uint32).view(np.int32).copy())
+                    self._copy_rows(steps.to(self.device), table.step, None, rows, n)
+                elif isinstance(table.optimizer, RowWiseAdagrad):
+                    self._copy_rows(torch.from_numpy(state[:, :1].copy()).to(self.device), table.state0, None, rows, n)
+        self.stream.synchronize()
+
+    def assign(self, keys: Any, values: Any) -> None:
+        """Sets the rows of ``keys`` (inserting them in a dynamic store) to ``values [n, dim]``."""
+        with torch.cuda.stream(self.stream):
+            v = to_device(values, self.device)
+            if v.dim() != 2:
+                raise ValueError(f"assign needs values of shape [keys, dim], got {tuple(v.shape)}")
+            table = self._table(int(v.shape[1]))
+            k = self._keys(keys)
+            if v.shape[0] != k.numel():
+                raise ValueError(f"values shape {tuple(v.shape)} does not match {k.numel()} keys")
+            rows = self._rows_of(k, table.dim, insert=True)
+            self._copy_rows(contiguous(v.to(table.table.dtype)), table.table, None, rows, int(k.numel()))
+
     # -- async forms (work is enqueued on the store's stream either way) ------
     async def async_lookup_or_insert(self, keys: Any, dim: int):
         return self.lookup_or_insert(keys, dim)
@@ -479,6 +597,24 @@ class DynamicEmbeddingStore(EmbeddingStore):
                              new.slots, int(self.stream.cuda_stream))
                 self.maps[int(dim)] = new
         self.capacity = max(self.capacity, capacity)
+
+    def _rows_of(self, keys: torch.Tensor, dim: int, insert: bool) -> torch.Tensor:
+        return self._resolve(keys, dim, insert, values=False)[0]
+
+    def _stored(self, dim: int):
+        kmap = self.maps[int(dim)]
+        count = kmap.count()  # synchronizes
+        keys = torch.empty(max(count, 1), dtype=torch.int64, device=self.device)
+        rows = torch.empty(max(count, 1), dtype=torch.int32, device=self.device)
+        total = torch.empty(1, dtype=torch.int64, device=self.device)
+        nbytes = _native.library().flare_keymap_export_workspace_bytes(kmap.slots)
+        ws = self._map_workspace.get(nbytes)
+        _native.call("flare_keymap_export", kmap.buffer.data_ptr(), kmap.slots, keys.data_ptr(), rows.data_ptr(),
+                     total.data_ptr(), ws.data_ptr(), nbytes, int(self.stream.cuda_stream))
+        self.stream.synchronize()
+        if int(total.item()) != count:
+            raise RuntimeError(f"key map export found {int(total.item())} keys, expected {count}")
+        return keys[:count], rows[:count]
 
     # -- gradients are kept per row ----------------------------------------------
     def accumulate_gradients(self, keys: Any, grad: Any) -> None:

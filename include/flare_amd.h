@@ -321,6 +321,27 @@ int flare_keymap_lookup_or_insert(void *map, int64_t capacity, const int64_t *ke
 int flare_keymap_rehash(const void *src, int64_t src_capacity, void *dst,
                         int64_t dst_capacity, void *stream);
 
+/* The keys that hold rows and their rows, in slot order: keys_out (int64) and
+ * rows_out (int32) need room for every stored key; *count_out (device int64)
+ * gets their number.  The store's export_page_images
+ * (tests/runtime/test_sparse_storage_limits.py:62-79,
+ * tools/validation/audit_sparse_checkpoint.py:33-70) reads keys, values,
+ * optimizer states and steps through it. */
+size_t flare_keymap_export_workspace_bytes(int64_t capacity);
+int flare_keymap_export(const void *map, int64_t capacity, int64_t *keys_out,
+                        int32_t *rows_out, int64_t *count_out, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* dst[dst_index[i]] = src[src_index[i]] for i < n, rows of row_bytes bytes
+ * copied as they are (either index may be NULL: the identity).  Rows outside
+ * [0, src_rows) / [0, dst_rows) are skipped and set device error bit 1.  The
+ * stores' assign(keys, values) (test_sparse_checkpoint_audit.py:35-39) and
+ * page-image export / import move values, optimizer state and step counters
+ * with it. */
+int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_rows,
+                    int64_t row_bytes, const int32_t *src_index,
+                    const int32_t *dst_index, int64_t n, void *stream);
+
 /* Reads back and clears the device-side error word that kernels set: bit 1 an
  * out-of-range index (written as 0 / ignored) or invalid CSR offsets, bit 2 an
  * exhausted spin-wait guard, bit 4 a full key map or table, bit 8 a checked
