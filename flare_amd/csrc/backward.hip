@@ -288,6 +288,12 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
 constexpr int kPrepMaxBags = 4096;
 
 // Bags per prepare block: about 512 blocks (fewer histogram flushes), at most kPrepMaxBags bags each.
+constexpr int64_t kPerBagLength = 8;
+// In the per-bag walk: bags longer than kPrepWalk ids go to a block-wide walk
+// (at most kPrepLongBags of them per block; more are walked by their thread).
+constexpr int64_t kPrepWalk = 32;
+constexpr int kPrepLongBags = 256;
+
 int prep_bags_per_block(int64_t bags) {
   return static_cast<int>(std::min<int64_t>(kPrepMaxBags, std::max<int64_t>(64, ceil_div(bags, 512))));
 }
@@ -297,7 +303,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
-    float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int *err) {
+    float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int per_bag, int *err) {
   __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
@@ -322,12 +328,8 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
   const int64_t first = s_off[0];
   const int64_t last = s_off[nb];
   const uint32_t sentinel = static_cast<uint32_t>(key_limit);
-  for (int64_t i = first + threadIdx.x; i < last; i += 256) {
-    int lo = 0, hi = nb;  // find bag: s_off[lo] <= i < s_off[lo+1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= i) lo = mid; else hi = mid;
-    }
+  // occurrence i of block-local bag lo
+  auto emit = [&](int64_t i, int lo) {
     const int64_t bag = bag0 + lo;
     const int64_t t = bag / batch;
     const int64_t b = bag - t * batch;
@@ -343,6 +345,40 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     grad_row[i] = static_cast<uint32_t>(b * num_tables + t);
     if (aux) aux[i] = static_cast<float>(s_off[lo + 1] - s_off[lo]);
     add_histograms(s_hist, k, passes, digit);
+  };
+  if (per_bag) {
+    // short bags: one thread per bag walks its few occurrences (no search);
+    // bags longer than kPrepWalk are listed and then walked by the whole block
+    __shared__ int s_long[kPrepLongBags];
+    __shared__ int s_nlong;
+    if (threadIdx.x == 0) s_nlong = 0;
+    __syncthreads();
+    for (int lo = threadIdx.x; lo < nb; lo += 256) {
+      const int64_t b0 = s_off[lo], b1 = s_off[lo + 1];
+      if (b1 - b0 > kPrepWalk) {
+        const int slot = atomicAdd(&s_nlong, 1);
+        if (slot < kPrepLongBags) {
+          s_long[slot] = lo;
+          continue;
+        }
+      }
+      for (int64_t i = b0; i < b1; ++i) emit(i, lo);
+    }
+    __syncthreads();
+    const int nlong = s_nlong < kPrepLongBags ? s_nlong : kPrepLongBags;
+    for (int j = 0; j < nlong; ++j) {
+      const int lo = s_long[j];
+      for (int64_t i = s_off[lo] + threadIdx.x; i < s_off[lo + 1]; i += 256) emit(i, lo);
+    }
+  } else {
+    for (int64_t i = first + threadIdx.x; i < last; i += 256) {
+      int lo = 0, hi = nb;  // find bag: s_off[lo] <= i < s_off[lo+1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid] <= i) lo = mid; else hi = mid;
+      }
+      emit(i, lo);
+    }
   }
   __syncthreads();
   flush_histograms(s_hist, hist, passes, digit);
@@ -2016,16 +2052,18 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   const RadixPlan plan = radix_plan(bits_for(sentinel), 4);
   FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
   const int bpb = prep_bags_per_block(bags);
+  // bags of at most kPerBagLength ids on average are walked one thread per bag
+  const int per_bag = n <= kPerBagLength * bags ? 1 : 0;
   const int pgrid = static_cast<int>(ceil_div(bags, bpb));
   float *aux = pooling == FLARE_POOL_MEAN ? w.aux : nullptr;
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   return dedup_rows(w, plan, sentinel, err, s, &sorted, first_indices_out, unique_out,

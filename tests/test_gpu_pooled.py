@@ -301,3 +301,35 @@ def test_backward_rejects_invalid_offsets(gpu_device, no_device_errors):
     shard.synchronize()
     no_device_errors(0)
     assert not np.array_equal(_host(shard.table), table)
+
+@pytest.mark.parametrize("case", ["long_bags_listed", "more_long_bags_than_the_list"])
+def test_short_bag_prepare_with_long_bags(gpu_device, no_device_errors, case):
+    """Batches averaging at most 8 ids per bag take the per-bag walk in the dedup's prepare;
+    its long bags go to a block-wide walk, and past 256 of them in a block to their own thread."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    rng = np.random.default_rng(31)
+    if case == "long_bags_listed":
+        table_rows, batch, dim = [20, 35, 7], 2000, 16
+        lengths = rng.integers(0, 3, size=len(table_rows) * batch)
+        lengths[::50] = 200
+    else:
+        table_rows, batch, dim = [50], 600000, 8
+        lengths = rng.integers(0, 2, size=batch)
+        lengths[:1200:4] = 33  # 300 long bags inside the first prepare block
+    assert lengths.sum() <= 8 * lengths.size
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    ids = (rng.integers(0, 1 << 30, size=int(offsets[-1])) % np.asarray(table_rows)[bag_table]).astype(np.int64)
+    shard = PooledTableShard(table_rows, dim, value_dtype="float32", initializer=Uniform(-1.0, 1.0), seed=4)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    grad = rng.normal(0, 1, size=(batch, len(table_rows), dim)).astype(np.float32)
+    unique, inverse, first, g = shard.reduce_pooled_gradients(ids, offsets, batch, grad)
+    shard.synchronize()
+    eu, ei, ef, eg = O.pooled_grad_sums(ids, offsets, row_base, batch, dim, grad)
+    np.testing.assert_array_equal(unique.cpu().numpy(), eu)
+    np.testing.assert_array_equal(inverse.cpu().numpy(), ei)
+    np.testing.assert_array_equal(first.cpu().numpy(), ef)
+    np.testing.assert_array_equal(g.cpu().numpy(), eg)
+    no_device_errors()
