@@ -189,6 +189,13 @@ def keymap_main(args) -> int:
         keys = keys[keys != np.iinfo(np.int64).min]
         key_sets.append(torch.from_numpy(keys.copy()).to(device))
     total = len(torch.unique(torch.cat(key_sets)))
+    # load every kernel of the path once (a separate small store), so the timed first insert
+    # does not include code-object loading
+    warm = DynamicEmbeddingStore(4096, [dim], value_dtype="bfloat16", optimizer=Sgd(), seed=4)
+    warm.lookup_or_insert(key_sets[0][:1000], dim)
+    warm.lookup_or_insert(key_sets[0][:1000], dim)
+    warm.synchronize()
+    del warm
     store = DynamicEmbeddingStore(total + 1024, [dim], value_dtype="bfloat16", optimizer=Sgd(), seed=3)
     stream = store.stream
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
