@@ -75,6 +75,7 @@ SIGNATURES = {
     "flare_keymap_export_workspace_bytes": (_sz, [_i64]),
     "flare_keymap_export": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "flare_copy_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "flare_nested_global_positions": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "flare_take_device_errors": (_i32, [_vp]),
 }
 

@@ -342,6 +342,22 @@ int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_ro
                     int64_t row_bytes, const int32_t *src_index,
                     const int32_t *dst_index, int64_t n, void *stream);
 
+/* Dense global positions (int32) of the unique ids' first occurrences in a
+ * ragged batch: _unique_global_flat_positions
+ * (src/flare/runtime/fluxway/workers/sparse_input.py:85-113) on the device.
+ * splits[k] (device int64, split_lengths[k] values) for k < levels <= 4:
+ * splits[0] maps local rows to level-1 entries, the last level maps entries
+ * to flat values.  Flat index first_indices[u] with path (r0, j1..jL) goes to
+ * origin_indices[r0] * S_0 + sum_k j_k * S_k, S the suffix products of widths
+ * (the dense shape after the row axis, host int64[levels]).  A path outside
+ * the splits, a j_k >= widths[k-1] or r0 >= origin_rows gives -1 and sets
+ * device error bit 1. */
+int flare_nested_global_positions(const int64_t *first_indices, int64_t count,
+                                  int32_t levels, const int64_t *const *splits,
+                                  const int64_t *split_lengths,
+                                  const int64_t *origin_indices, int64_t origin_rows,
+                                  const int64_t *widths, int32_t *out, void *stream);
+
 /* Reads back and clears the device-side error word that kernels set: bit 1 an
  * out-of-range index (written as 0 / ignored) or invalid CSR offsets, bit 2 an
  * exhausted spin-wait guard, bit 4 a full key map or table, bit 8 a checked

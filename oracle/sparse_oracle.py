@@ -29,6 +29,8 @@ How each part is pinned (tests/test_oracle.py, tests/test_golden.py):
 * rowwise_adagrad_update: the optax closed form it reduces to at D == 1 and
   the row mean of squares.
 * sgd_update: the flush-window known answer.
+* nested_global_positions: the reference's vector (test_sparse_input_resources.py:77-105) and
+  a brute force that lays ragged batches out densely.
 * KeyMap (the dynamic store's key -> row map): a dict restatement of
   first-occurrence row assignment, checked by closed-form sequences and
   invariants; its mixing function splitmix64 by the published SplitMix64
@@ -643,6 +645,38 @@ def storage_ulp_distance(a, b, storage: str) -> np.ndarray:
     def key(i):
         return np.where(i & 0x8000, -(i & 0x7FFF), i)
     return np.abs(key(ia) - key(ib))
+
+
+# --------------------------------------------------------------------------
+# CSR-native ingest: dense positions of first occurrences
+# (_unique_global_flat_positions, sparse_input.py:85-113; its helpers live in the
+# absent fluxway.common.tensor_components, so this states the row-major offset of
+# each flat value's nested path, pinned by the reference's vector
+# tests/runtime/test_sparse_input_resources.py:77-105 and a dense brute force)
+# --------------------------------------------------------------------------
+def nested_global_positions(nested_splits, first_indices, widths, origin_indices) -> np.ndarray:
+    """Flat index -> (row r0, j1..jL) -> origin[r0]*S0 + sum j_k*S_k (S: suffix products of
+    widths); -1 where the path leaves the dense shape."""
+    levels = len(nested_splits)
+    strides = [1] * (levels + 1)
+    for k in range(levels - 1, -1, -1):
+        strides[k] = strides[k + 1] * int(widths[k])
+    v = np.asarray(first_indices, dtype=np.int64).copy()
+    pos = np.zeros(v.size, dtype=np.int64)
+    ok = np.ones(v.size, dtype=bool)
+    for k in range(levels - 1, -1, -1):
+        sp = np.asarray(nested_splits[k], dtype=np.int64)
+        inside = (v >= sp[0]) & (v < sp[-1]) & ok
+        e = np.searchsorted(sp, v, side="right") - 1
+        e = np.clip(e, 0, max(sp.size - 2, 0))
+        j = v - sp[e]
+        ok &= inside & (j < int(widths[k]))
+        pos += np.where(ok, j * strides[k + 1], 0)
+        v = np.where(ok, e, 0)
+    origin = np.asarray(origin_indices, dtype=np.int64)
+    ok &= v < origin.size
+    pos += np.where(ok, origin[np.where(ok, v, 0)] * strides[0] if origin.size else 0, 0)
+    return np.where(ok, pos, -1).astype(np.int32)
 
 
 # --------------------------------------------------------------------------
