@@ -102,3 +102,33 @@ def test_status_mapping():
         with pytest.raises(ValueError):
             _native.check(code)
     _native.check(_native.OK)
+
+
+def test_keymap_and_ingest_validation_on_host():
+    lib = _native.library()
+    assert lib.flare_keymap_bytes(63) == 0 and lib.flare_keymap_bytes(100) == 0
+    assert lib.flare_keymap_bytes(64) == 256 + 64 * 16
+    assert lib.flare_keymap_bytes(1 << 31) == 0
+    assert lib.flare_keymap_workspace_bytes(-1) == 0 and lib.flare_keymap_workspace_bytes(10) > 0
+    assert lib.flare_keymap_export_workspace_bytes(128) > 0
+    status = _call("flare_keymap_init", None, 100, None)
+    assert status == _native.ERR_ARGUMENT and "power of two" in _native.last_error()
+    status = _call("flare_keymap_lookup_or_insert", None, 64, None, 4, 1, None, _native.FLOAT32, 10, 8,
+                   0.0, 1.0, 0, None, None, None, 0, None)
+    assert status == _native.ERR_ARGUMENT  # null map
+    status = _call("flare_nested_global_positions", None, 3, 0, None, None, None, 0, None, None, None)
+    assert status == _native.ERR_ARGUMENT and "nested levels" in _native.last_error()
+    status = _call("flare_copy_rows", None, 4, None, 4, 3, None, None, 1, None)
+    assert status == _native.ERR_SHAPE
+
+
+def test_gradient_transport_dtype_validation_on_host():
+    opt = _native.FlareOptimizer()
+    opt.kind = _native.OPT_SGD
+    status = _call("flare_sparse_update_ex", None, _native.FLOAT32, 10, 4, None, None, None, ctypes.byref(opt),
+                   None, 1, None, _native.FLOAT16, 0, None, 1, None, 0, None)
+    assert status == _native.ERR_DTYPE and "gradient_transport_dtype" in _native.last_error()
+    with pytest.raises(TypeError, match="gradient_transport_dtype"):
+        _native.check(status)
+    status = _call("flare_check_finite", None, _native.FLOAT32, -1, None, None)
+    assert status == _native.ERR_SHAPE
