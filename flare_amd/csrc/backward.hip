@@ -1016,6 +1016,11 @@ constexpr uint32_t kInlineSpan = 8;
 // Lane groups launched for apply_kernel at most: fewer, busier blocks beat
 // one block per 8 keys once there are more keys than the GPU holds at once.
 constexpr int64_t kApplyGroups = 131072;
+// A hot key spanning more than kFoldChunk units is folded in two levels: each
+// run of kFoldChunk consecutive unit partials left to right (in parallel over
+// the runs, fold_chunks_kernel), then the run results left to right
+// (fold_kernel).  Keys of up to kFoldChunk units are folded left to right.
+constexpr uint32_t kFoldChunk = 64;
 // Partial rows per lane group and fold round (at most; fewer for wide rows).
 constexpr int kFoldDepth = 16;
 
@@ -1373,6 +1378,89 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
   }
 }
 
+// Unit partials of key r: piece 0 is the first unit's slot 1, piece p > 0 the
+// slot 0 of unit h + p.
+__device__ __forceinline__ float *piece_row(const UpdateArgs &a, uint32_t h, uint32_t p) {
+  return a.partial + (static_cast<size_t>(h + p) * 2 + (p == 0 ? 1 : 0)) * a.dim;
+}
+
+// First level of the fold of keys with more than kFoldChunk pieces: one lane
+// group per run of kFoldChunk pieces sums them left to right and writes the
+// result over the run's first piece.  Work items: every unit (the run that
+// starts there, for runs after a key's first) and every hot key (its first
+// run).
+template <int VEC, int G, int NC>
+__global__ __launch_bounds__(256) void fold_chunks_kernel(UpdateArgs a) {
+  if (a.reject && *a.reject) return;
+  constexpr int kGroups = 256 / G;
+  constexpr int kAhead = kFoldDepth / NC;
+  const int lane = threadIdx.x % G;
+  const int D = a.dim;
+  const uint32_t nvalid = a.meta[0];
+  const uint32_t hot = a.meta[2];
+  const uint32_t items = a.units + hot;
+  for (uint32_t w = blockIdx.x * kGroups + threadIdx.x / G; w < items; w += gridDim.x * kGroups) {
+    uint32_t r, first;
+    if (w < a.units) {
+      if (w * kReduceUnit >= nvalid) continue;
+      r = a.unit_first_run[w];
+      if (a.run_start[r] >= w * kReduceUnit) continue;  // the unit's first key starts in it
+      first = w - a.run_start[r] / kReduceUnit;
+      if (first % kFoldChunk != 0) continue;
+    } else {
+      r = a.hot_runs[w - a.units];
+      first = 0;
+    }
+    const uint32_t seg_start = a.run_start[r];
+    const uint32_t seg_end = a.run_start[r + 1];
+    if (seg_end <= seg_start || seg_end > a.n) continue;
+    const uint32_t h = seg_start / kReduceUnit;
+    const uint32_t count = (seg_end - 1) / kReduceUnit - h + 1;
+    if (count <= kFoldChunk) continue;  // one level: fold_kernel
+    const uint32_t m = min(kFoldChunk, count - first);
+    float g[NC][VEC];
+    const float *seed = piece_row(a, h, first);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (col < D) load_f32<VEC>(seed + col, g[c]);
+    }
+    for (uint32_t k = 1; k < m; k += kAhead) {  // kAhead rows in flight, added in order
+      float y[kAhead][NC][VEC];
+#pragma unroll
+      for (int t = 0; t < kAhead; ++t) {
+        const bool ok = k + t < m;
+        const float *src = piece_row(a, h, first + (ok ? k + t : 0));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = (c * G + lane) * VEC;
+          if (ok && col < D) {
+            load_f32<VEC>(src + col, y[t][c]);
+          } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) y[t][c][v] = 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kAhead; ++t) {
+        if (k + t < m) {  // predicated, so the rows stay in registers
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) g[c][v] += y[t][c][v];
+        }
+      }
+    }
+    float *dst = piece_row(a, h, first);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * G + lane) * VEC;
+      if (col < D) store_f32<VEC>(dst + col, g[c]);
+    }
+  }
+}
+
 // Hot keys: one block per key folds the key's unit partials in order.  Each
 // round the block's lane groups load up to kFoldDepth partial rows each into LDS
 // (all loads in flight together), then group 0 adds them left to right: the
@@ -1396,7 +1484,12 @@ __global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
     if (seg_end <= seg_start || seg_end > a.n) continue;  // block-uniform
     const uint32_t h = seg_start / kReduceUnit;
     const uint32_t last = (seg_end - 1) / kReduceUnit;
-    const uint32_t count = last - h + 1;  // partial rows to fold, in order
+    const uint32_t pieces = last - h + 1;
+    // rows to fold, in order: the pieces, or the results of fold_chunks_kernel
+    // (one per run of kFoldChunk pieces, over the run's first piece)
+    const bool chunked = pieces > kFoldChunk;
+    const uint32_t count = chunked ? (pieces + kFoldChunk - 1) / kFoldChunk : pieces;
+    const uint32_t stride = chunked ? kFoldChunk : 1;
     RowAhead<NC, VEC> ahead;
     float g[NC][VEC];
 #pragma unroll
@@ -1412,7 +1505,7 @@ __global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
       for (int t = 0; t < kDepthMax; ++t) {
         const uint32_t k = base + group * depth + t;
         const bool ok = t < depth && k < count;
-        const float *src = a.partial + (static_cast<size_t>(h + (ok ? k : 0)) * 2 + (k == 0 ? 1 : 0)) * D;
+        const float *src = piece_row(a, h, ok ? k * stride : 0);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           const int col = (c * G + lane) * VEC;
@@ -1434,6 +1527,14 @@ __global__ __launch_bounds__(256) void fold_kernel(UpdateArgs a, int depth) {
       if (group == 0) {
         const uint32_t m = min(chunk, count - base);
         uint32_t k = 0;
+        if (base == 0) {  // the first row seeds the sum
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int col = (c * G + lane) * VEC;
+            if (col < D) load_f32<VEC>(s_rows + col, g[c]);
+          }
+          k = 1;
+        }
         for (; k + 8 <= m; k += 8) {  // eight LDS rows read ahead of the in-order adds
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
@@ -1514,9 +1615,16 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   };
   auto fold_lds = [&](int g) { return static_cast<size_t>(256 / g) * fold_depth(g) * a.dim * 4; };
   const int fold_grid = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(a.units, kInlineSpan + 1))));
+  // fold_chunks: one work item per unit plus one per hot key (at most one per
+  // kInlineSpan + 1 units); the grid strides over them
+  auto chunk_grid = [&](int g) {
+    const int64_t items = static_cast<int64_t>(a.units) + a.units / (kInlineSpan + 1) + 1;
+    return static_cast<int>(std::min<int64_t>(16384, std::max<int64_t>(1, ceil_div(items, 256 / g))));
+  };
 #define FLARE_UPDATE_PAIR(G_, NC_)                                                          \
   if (a.grad_bf16) sums_kernel<Tag, VEC, G_, NC_, MODE, true><<<grid(G_), 256, 0, s>>>(a);  \
   else sums_kernel<Tag, VEC, G_, NC_, MODE, false><<<grid(G_), 256, 0, s>>>(a);            \
+  fold_chunks_kernel<VEC, G_, NC_><<<chunk_grid(G_), 256, 0, s>>>(a);                       \
   fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
   if (a.grad_bf16) apply_kernel<Tag, VEC, G_, NC_, MODE, true><<<apply_grid(G_), 256, 0, s>>>(a); \
   else apply_kernel<Tag, VEC, G_, NC_, MODE, false><<<apply_grid(G_), 256, 0, s>>>(a);

@@ -361,8 +361,10 @@ def materialize_padded_inverse_csr(ids, offsets, batch_size, max_elements, pad_i
 # key and reduces each key's occurrences in occurrence order, cut into fixed
 # "units" of REDUCE_UNIT consecutive sorted positions: a key's occurrences are
 # summed sequentially inside each unit, and the unit partials are then folded
-# left to right.  A key whose occurrences fall in one unit is summed exactly
-# in slot order, i.e. bit-identically to the Numba reference.
+# left to right; a key of more than FOLD_CHUNK unit partials folds each run of
+# FOLD_CHUNK partials left to right, then the run results left to right (so a
+# very hot key's fold is parallel).  A key whose occurrences fall in one unit
+# is summed exactly in slot order, i.e. bit-identically to the Numba reference.
 # --------------------------------------------------------------------------
 
 REDUCE_UNIT = 64
@@ -383,6 +385,9 @@ def sorted_occurrences(keys: np.ndarray, valid: np.ndarray | None = None):
         heads = np.zeros(0, dtype=bool)
     starts = np.nonzero(heads)[0]
     return perm, sk, starts
+
+
+FOLD_CHUNK = 64  # unit partials per first-level fold run of a very hot key
 
 
 def segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int, unit: int = REDUCE_UNIT):
@@ -416,14 +421,28 @@ def segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int, unit: int 
     for step in range(int(plen.max())):
         act = np.nonzero(plen > step)[0]
         partial[act] = (partial[act] + contrib[pa[act] + step]).astype(np.float32)
-    # fold pieces of each segment left to right (first piece is the seed)
+    # fold pieces of each segment left to right (first piece is the seed); a
+    # segment of more than FOLD_CHUNK pieces folds each run of FOLD_CHUNK pieces
+    # left to right, then the run results left to right
     first_piece = np.ones(pa.size, dtype=bool)
     first_piece[1:] = piece_seg[1:] != piece_seg[:-1]
     out[piece_seg[first_piece]] = partial[first_piece]
-    rest = np.nonzero(~first_piece)[0]
-    for p in rest:  # few: only keys crossing a unit boundary
-        s = piece_seg[p]
-        out[s] = (out[s] + partial[p]).astype(np.float32)
+    heads = np.nonzero(first_piece)[0]
+    counts = np.diff(np.append(heads, pa.size))
+    for s0, c in zip(heads[counts > 1].tolist(), counts[counts > 1].tolist()):  # keys crossing units
+        seg = piece_seg[s0]
+        if c <= FOLD_CHUNK:
+            acc = partial[s0].copy()
+            for p in range(s0 + 1, s0 + c):
+                acc = (acc + partial[p]).astype(np.float32)
+        else:
+            acc = None
+            for c0 in range(0, c, FOLD_CHUNK):
+                run = partial[s0 + c0].copy()
+                for p in range(s0 + c0 + 1, s0 + min(c0 + FOLD_CHUNK, c)):
+                    run = (run + partial[p]).astype(np.float32)
+                acc = run if acc is None else (acc + run).astype(np.float32)
+        out[seg] = acc
     return out
 
 

@@ -212,3 +212,29 @@ def test_scatter_hot_key_across_many_units_bit_exact(gpu_device, no_device_error
     op.stream.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), O.scatter(rows, dim, inverse, rows, grad))
     no_device_errors()
+
+
+@pytest.mark.parametrize("dim", [4, 128, 300, 2048])
+def test_scatter_key_past_the_fold_chunk_bit_exact(gpu_device, no_device_errors, dim):
+    """Keys spanning more than 64 units (two-level fold: runs of 64 unit partials folded in
+    parallel, then the runs) and one spanning exactly 64, against the oracle bit for bit."""
+    op = _op()
+    rng = np.random.default_rng(500 + dim)
+    rows = 40
+    slots = 64 * 64 * 3 + 777
+    inverse = rng.integers(0, rows + 1, slots).astype(np.int32)  # rows == pad
+    pick = rng.random(slots)
+    inverse[pick < 0.55] = 3        # ~6.9K occurrences: ~110 units
+    inverse[(pick >= 0.55) & (pick < 0.85)] = 11
+    grad = rng.standard_normal((slots, dim)).astype(np.float32)
+    out = op.scatter(rows, dim, torch.from_numpy(inverse).to(gpu_device), rows,
+                     torch.from_numpy(grad).to(gpu_device))
+    op.stream.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), O.scatter(rows, dim, inverse, rows, grad))
+    # exactly 64 units for one key: the one-level fold
+    inv2 = np.full(64 * 64, 5, np.int32)
+    g2 = rng.standard_normal((inv2.size, dim)).astype(np.float32)
+    out2 = op.scatter(rows, dim, torch.from_numpy(inv2).to(gpu_device), rows, torch.from_numpy(g2).to(gpu_device))
+    op.stream.synchronize()
+    np.testing.assert_array_equal(out2.cpu().numpy(), O.scatter(rows, dim, inv2, rows, g2))
+    no_device_errors()

@@ -333,3 +333,27 @@ def test_short_bag_prepare_with_long_bags(gpu_device, no_device_errors, case):
     np.testing.assert_array_equal(first.cpu().numpy(), ef)
     np.testing.assert_array_equal(g.cpu().numpy(), eg)
     no_device_errors()
+
+
+def test_pooled_step_with_a_key_past_the_fold_chunk(gpu_device, no_device_errors):
+    """Row-wise Adagrad through the fused path when one key holds ~60% of 20K occurrences."""
+    from flare_amd.store import PooledTableShard, RowWiseAdagrad, Uniform
+
+    rng = np.random.default_rng(41)
+    table_rows, batch, dim = [30, 9], 10000, 64
+    ids = rng.integers(0, 9, size=2 * batch).astype(np.int64)
+    ids[:batch][rng.random(batch) < 0.6] = 4   # hot key of table 0: ~6K occurrences, ~94 units
+    ids[:batch] = np.where(ids[:batch] < 30, ids[:batch], 0)
+    offsets = np.arange(2 * batch + 1, dtype=np.int64)
+    shard = PooledTableShard(table_rows, dim, value_dtype="float32", optimizer=RowWiseAdagrad(lr=0.01),
+                             initializer=Uniform(-1.0, 1.0), seed=8)
+    table0 = shard.table.clone().cpu().numpy()
+    grad = rng.normal(0, 1e-2, size=(batch, 2, dim)).astype(np.float32)
+    shard.apply_pooled_gradients(ids, offsets, batch, grad)
+    shard.synchronize()
+    row_base = np.asarray([0, 30, 39], np.int64)
+    _, e_table, e_state, *_ = O.pooled_step(table0, {"acc": np.zeros(39, np.float32)}, ids, offsets, row_base,
+                                             batch, dim, grad, storage="float32")
+    assert O.storage_ulp_distance(shard.table.cpu().numpy(), e_table, "float32").max() <= 1
+    np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["acc"], rtol=1e-5)
+    no_device_errors()

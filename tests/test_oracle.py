@@ -313,3 +313,45 @@ def test_pooled_step_equals_composed_reference_ops():
     untouched = np.setdiff1d(np.arange(w.total_rows), eu)
     np.testing.assert_array_equal(new_table[untouched], table[untouched])
     assert got.shape == (eu.size, w.dim) and pooled.shape == (w.batch, w.num_tables, w.dim)
+
+
+def test_segment_sums_two_level_fold_keeps_every_term():
+    """A key of more than FOLD_CHUNK unit pieces is folded in runs of FOLD_CHUNK, then the runs:
+    integer-valued rows sum exactly in any order, so every piece must be counted once."""
+    rng = np.random.default_rng(77)
+    unit = O.REDUCE_UNIT
+    total = unit * (2 * O.FOLD_CHUNK + 5) + 17
+    starts = np.asarray([0, 3, total - 40])  # the middle key spans 133 units
+    contrib = rng.integers(-8, 9, size=(total, 5)).astype(np.float32)
+    out = O.segment_sums(contrib, starts, total)
+    ends = np.append(starts[1:], total)
+    for s, (a, e) in enumerate(zip(starts, ends)):
+        np.testing.assert_array_equal(out[s], contrib[a:e].astype(np.float64).sum(axis=0).astype(np.float32))
+
+
+def test_segment_sums_fold_order_changes_only_past_fold_chunk():
+    rng = np.random.default_rng(78)
+    unit = O.REDUCE_UNIT
+    for units in (O.FOLD_CHUNK, O.FOLD_CHUNK + 1):
+        total = unit * units
+        contrib = (rng.standard_normal((total, 3)) * np.float32(1e3)).astype(np.float32)
+        starts = np.asarray([0])
+        out = O.segment_sums(contrib, starts, total)
+        pieces = [contrib[u * unit:(u + 1) * unit] for u in range(units)]
+        sums = []
+        for p in pieces:  # sequential inside each unit, seeded by zero
+            acc = np.zeros(3, np.float32)
+            for row in p:
+                acc = (acc + row).astype(np.float32)
+            sums.append(acc)
+        flat = sums[0]
+        for x in sums[1:]:
+            flat = (flat + x).astype(np.float32)
+        if units <= O.FOLD_CHUNK:
+            np.testing.assert_array_equal(out[0], flat)
+        else:
+            run0 = sums[0]
+            for x in sums[1:O.FOLD_CHUNK]:
+                run0 = (run0 + x).astype(np.float32)
+            expected = (run0 + sums[O.FOLD_CHUNK]).astype(np.float32)
+            np.testing.assert_array_equal(out[0], expected)
