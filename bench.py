@@ -22,6 +22,7 @@ build measures one GPU.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -72,20 +73,52 @@ def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weight
     return fwd, bwd, update
 
 
-def pooled_kernel_traffic(config: int):
-    """HBM bytes per pooled_kernel launch from the committed counter runs, or None.
+def update_kernel_bytes(keys, dim: int, s: int, optimizer: str) -> tuple[int, int]:
+    """Algorithmic HBM bytes of the two update kernels for one batch of global row keys.
 
-    profiles/pooled_kernel_traffic.json holds FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch) of the pooled gather on this workload and the factors that map
+    Keys are stably sorted; a key is "long" when its sorted positions cross a 64-position
+    unit boundary or number more than 4 (those are summed by sums_kernel, one partial row per
+    unit piece), else "short" (summed inside apply_kernel).
+    sums_kernel : N_long * (D*4 gradient row + 4 row index) + P_long * D*4 partial rows
+    apply_kernel: U * (2*D*s row read and write + 2*S state) + N_short * (D*4 + 4)
+                  + U_long * D*4 (the long key's folded sum)
+    """
+    import numpy as np
+
+    _, counts = np.unique(keys, return_counts=True)
+    starts = np.cumsum(counts) - counts
+    h = starts // 64
+    last = (starts + counts - 1) // 64
+    long_ = (h != last) | (counts > 4)
+    n_long = int(counts[long_].sum())
+    p_long = int((last - h + 1)[long_].sum())
+    u, u_long = int(counts.size), int(long_.sum())
+    n_short = int(counts.sum()) - n_long
+    if optimizer == "none":
+        rows_state = u * dim * 4
+    else:
+        state = 2 * dim * 4 + 4 if optimizer == "adam" else STATE_BYTES[optimizer]
+        rows_state = 2 * u * dim * s + 2 * u * state
+    sums = n_long * (dim * 4 + 4) + p_long * dim * 4
+    apply = rows_state + n_short * (dim * 4 + 4) + u_long * dim * 4
+    return sums, apply
+
+
+def kernel_traffic(config: int, kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter runs, or None.
+
+    profiles/step_kernel_traffic.json holds FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch) of the step's kernels on one workload and the factors that map
     each counter onto the bytes of a plain device copy of known size.
     """
-    path = ROOT / "profiles" / "pooled_kernel_traffic.json"
+    path = ROOT / "profiles" / "step_kernel_traffic.json"
     if not path.exists():
         return None
     rec = json.loads(path.read_text())
-    if rec.get("workload_id") != config:
+    k = rec.get("kernels", {}).get(kernel)
+    if rec.get("workload_id") != config or k is None:
         return None
-    return (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024.0
+    return (k["fetch_kib"] * rec["fetch_scale"] + k["write_kib"] * rec["write_scale"]) * 1024.0
 
 
 def _cpu_inputs(w):
@@ -160,6 +193,218 @@ def cpu_baseline(config: int, seconds: float) -> dict:
     }
 
 
+def _int64_key_sets(batches: int) -> list:
+    """Unique ids of workload 5 batches (1e8-id space, 131072 bags of U[1,64] Zipf(1.05) ids)
+    in first-occurrence order, mixed by the SplitMix64 output function into arbitrary int64
+    keys (numpy arrays)."""
+    import numpy as np
+
+    from flare_amd.workload import make_workload
+
+    out = []
+    for k in range(batches):
+        ids = make_workload(5, batch_index=k).ids
+        _, first = np.unique(ids, return_index=True)
+        uids = ids[np.sort(first)].astype(np.uint64)
+        with np.errstate(over="ignore"):
+            z = (uids ^ (uids >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+            z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+            z = z ^ (z >> np.uint64(31))
+        keys = z.view(np.int64)
+        out.append(keys[keys != np.iinfo(np.int64).min].copy())
+    return out
+
+
+def _event_ms(stream, fn, steps: int, warmup: int) -> float:
+    """Median over ``steps`` calls of ``fn`` of the time between events recorded on ``stream``
+    around each call (after ``warmup`` untimed calls)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in events:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in events)
+
+
+def ingest_main(args) -> int:
+    """CSR-native ingest: dense global positions of each unique id's first occurrence.
+
+    One ragged feature of workload 5 (131072 rows of U[1,64] ids, dense width 64): the first
+    occurrences of its unique ids (about 1.1M of 4.3M) are mapped through the row splits and
+    the rows' origins (``origin_indices``: this worker's rows at offset 131072 of the global
+    batch) to ``origin*64 + j``.  A second line runs a two-level nesting (rows of up to 8
+    lists of up to 8 ids) of the same ids.
+    """
+    import numpy as np
+    import torch
+
+    from flare_amd import _native
+    from flare_amd.workload import make_workload
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    w = make_workload(5)
+    ids = w.ids
+    _, first = np.unique(ids, return_index=True)
+    first = np.sort(first).astype(np.int64)
+    rows = w.batch
+    origin = (np.arange(rows, dtype=np.int64) + rows)
+    # two levels: each bag of <= 64 ids split into lists of <= 8
+    lengths = np.diff(w.offsets)
+    inner = []
+    outer = np.zeros(rows + 1, np.int64)
+    for b, ln in enumerate(lengths.tolist()):
+        parts = [8] * (ln // 8) + ([ln % 8] if ln % 8 else [])
+        inner.extend(parts)
+        outer[b + 1] = outer[b] + len(parts)
+    inner_splits = np.zeros(len(inner) + 1, np.int64)
+    inner_splits[1:] = np.cumsum(inner)
+    cases = [("1 level, width 64", [np.asarray(w.offsets, np.int64)], [64]),
+             ("2 levels, widths 8 x 8", [outer, inner_splits], [8, 8])]
+    stream = torch.cuda.Stream(device)
+    for name, splits, widths in cases:
+        d_splits = [torch.from_numpy(sp).to(device) for sp in splits]
+        d_first = torch.from_numpy(first).to(device)
+        d_origin = torch.from_numpy(origin).to(device)
+        out = torch.empty(first.size, dtype=torch.int32, device=device)
+        levels = len(splits)
+        ptrs = (ctypes.c_void_p * levels)(*[t.data_ptr() for t in d_splits])
+        lens = (ctypes.c_int64 * levels)(*[int(t.numel()) for t in d_splits])
+        dims = (ctypes.c_int64 * levels)(*widths)
+
+        def call():
+            _native.call("flare_nested_global_positions", d_first.data_ptr(), int(first.size), levels,
+                         ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(lens, ctypes.c_void_p),
+                         d_origin.data_ptr(), int(origin.size), ctypes.cast(dims, ctypes.c_void_p),
+                         out.data_ptr(), int(stream.cuda_stream))
+
+        ms = _event_ms(stream, call, args.steps, args.warmup)
+        got = out.cpu().numpy()
+        # algorithmic bytes: each first index read (8) and position written (4), one origin
+        # read (8) and, per level, the two split entries that bound its list (16)
+        per_index = 8 + 4 + 8 + 16 * levels
+        gbs = first.size * per_index / (ms * 1e-3) / 1e9
+        line = {
+            "metric": "nested global positions per second (CSR-native ingest)",
+            "value": first.size / (ms * 1e-3),
+            "unit": "positions/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_call": ms,
+            "higher_is_better": True, "dtype": "int64",
+            "data": "synthetic (workload 5 ids)",
+            "config": {"workload": f"{first.size} first occurrences of {ids.size} ids in {rows} rows, {name}"},
+            "roofline": {"kernel": "positions_kernel", "bound": "hbm", "achieved": gbs, "peak": 8000.0,
+                         "unit": "GB/s", "frac": gbs / 8000.0, "traffic": None,
+                         "algorithmic_bytes_per_position": per_index},
+        }
+        if not args.no_cpu_baseline:
+            from oracle import sparse_oracle as O  # the CPU leg only
+
+            t0 = time.perf_counter()
+            reps = 0
+            while True:
+                exp = O.nested_global_positions(splits, first, widths, origin)
+                reps += 1
+                if time.perf_counter() - t0 > 3.0 or reps >= 20:
+                    break
+            cpu_s = (time.perf_counter() - t0) / reps
+            if not np.array_equal(exp, got):
+                raise SystemExit(f"ingest positions differ from the oracle ({name})")
+            line["cpu_baseline"] = {"value": first.size / cpu_s, "unit": "positions/s", "cores": 1,
+                                    "kind": "port", "sample": f"the same input, numpy, {reps} calls"}
+        print(json.dumps(line), flush=True)
+    return 0
+
+
+def pages_main(args) -> int:
+    """Checkpoint page images of a dynamic store: export and import of every stored row.
+
+    A 128-wide bf16 table under Adam holds the int64 keys of four workload 5 batches (about
+    4M keys).  The device part of an export is the key map export plus the gathers of values,
+    ``m``, ``v`` and step counters into page buffers; of an import, the key lookup plus the
+    scatters back.  Both are timed with events; the whole ``export_page_images`` /
+    ``import_page_images`` calls (pages of 1M keys, host numpy arrays: PCIe-inclusive) are
+    timed by the wall clock beside them.
+    """
+    import numpy as np
+    import torch
+
+    from flare_amd.conversion import contiguous
+    from flare_amd.store import Adam, DynamicEmbeddingStore
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    dim = 128
+    keys = np.unique(np.concatenate(_int64_key_sets(4)))
+    store = DynamicEmbeddingStore(int(keys.size) + 1024, [dim], value_dtype="bfloat16", optimizer=Adam(), seed=5)
+    d_keys = torch.from_numpy(keys).to(device)
+    for lo in range(0, keys.size, 1 << 20):
+        store.lookup_or_insert(d_keys[lo:lo + (1 << 20)], dim)
+    store.synchronize()
+    table = store.tables[dim]
+    n = store.size(dim)
+    stream = store.stream
+    values = torch.empty((n, dim), dtype=table.table.dtype, device=device)
+    m = torch.empty((n, dim), dtype=torch.float32, device=device)
+    v = torch.empty((n, dim), dtype=torch.float32, device=device)
+    steps = torch.empty(n, dtype=torch.int32, device=device)
+    stored = {}
+
+    def export_device():
+        with torch.cuda.stream(stream):
+            k, rows = store._stored(dim)
+            stored["keys"], stored["rows"] = k, contiguous(rows)
+            store._copy_rows(table.table, values, stored["rows"], None, n)
+            store._copy_rows(table.state0, m, stored["rows"], None, n)
+            store._copy_rows(table.state1, v, stored["rows"], None, n)
+            store._copy_rows(table.step, steps, stored["rows"], None, n)
+
+    def import_device():
+        with torch.cuda.stream(stream):
+            rows = store._rows_of(stored["keys"], dim, insert=True)
+            store._copy_rows(values, table.table, None, rows, n)
+            store._copy_rows(m, table.state0, None, rows, n)
+            store._copy_rows(v, table.state1, None, rows, n)
+            store._copy_rows(steps, table.step, None, rows, n)
+
+    export_ms = _event_ms(stream, export_device, args.steps, args.warmup)
+    import_ms = _event_ms(stream, import_device, args.steps, args.warmup)
+    t0 = time.perf_counter()
+    pages = store.export_page_images()
+    export_wall = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    store.import_page_images(pages)
+    import_wall = time.perf_counter() - t0
+    slots = store.maps[dim].slots
+    # per key: value row 2*256 B (read + write), m and v 2*512 B each, step 2*4 B; the export
+    # also writes key (8) and row (4) and reads every map slot (16 B) once, the import reads
+    # the key (8), probes its slot (16) and writes the row (4)
+    row_bytes = 2 * (dim * 2 + 2 * dim * 4 + 4)
+    export_bytes = n * (row_bytes + 12) + 16 * slots
+    import_bytes = n * (row_bytes + 28)
+    for name, ms, nbytes, wall in (("export", export_ms, export_bytes, export_wall),
+                                   ("import", import_ms, import_bytes, import_wall)):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": f"checkpoint page image {name} rows/s (device part)",
+            "value": n / (ms * 1e-3), "unit": "rows/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_call": ms,
+            "higher_is_better": True, "dtype": "bf16 rows, fp32 Adam state",
+            "data": "synthetic (workload 5 unique ids of 4 batches as int64 keys)",
+            "config": {"workload": f"{n} keys, 128-wide bf16 table, Adam, map of {slots} slots"},
+            "host_inclusive_s": wall, "host_inclusive_rows_per_s": n / wall,
+            "roofline": {"kernel": "whole device part", "bound": "hbm", "achieved": gbs, "peak": 8000.0,
+                         "unit": "GB/s", "frac": gbs / 8000.0, "traffic": None,
+                         "algorithmic_bytes": nbytes},
+        }), flush=True)
+    return 0
+
+
 def keymap_main(args) -> int:
     """Dynamic store: lookup_or_insert of one step's unique keys into a 128-wide bf16 table.
 
@@ -167,27 +412,14 @@ def keymap_main(args) -> int:
     Zipf(1.05) ids), in first-occurrence order, mixed into arbitrary int64 keys.  The first
     call inserts every key; the timed calls rotate over the batches once all are inserted.
     """
-    import numpy as np
     import torch
 
     from flare_amd.store import DynamicEmbeddingStore, Sgd
-    from flare_amd.workload import make_workload
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     dim, batches = 128, max(2, min(args.batches, 4))
-    key_sets = []
-    for k in range(batches):
-        ids = make_workload(5, batch_index=k).ids
-        _, first = np.unique(ids, return_index=True)
-        uids = ids[np.sort(first)].astype(np.uint64)
-        with np.errstate(over="ignore"):  # splitmix64 output function: ids -> arbitrary int64 keys
-            z = (uids ^ (uids >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-            z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-            z = z ^ (z >> np.uint64(31))
-        keys = z.view(np.int64)
-        keys = keys[keys != np.iinfo(np.int64).min]
-        key_sets.append(torch.from_numpy(keys.copy()).to(device))
+    key_sets = [torch.from_numpy(k).to(device) for k in _int64_key_sets(batches)]
     total = len(torch.unique(torch.cat(key_sets)))
     # load every kernel of the path once (a separate small store), so the timed first insert
     # does not include code-object loading
@@ -263,6 +495,10 @@ def main() -> int:
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
                     help="measure the dynamic store's key map (lookup_or_insert) instead of the pooled step")
+    ap.add_argument("--ingest", action="store_true",
+                    help="measure CSR-native ingest (nested global positions) instead of the pooled step")
+    ap.add_argument("--pages", action="store_true",
+                    help="measure checkpoint page image export/import instead of the pooled step")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -272,9 +508,14 @@ def main() -> int:
 
     if args.keymap:
         return keymap_main(args)
+    if args.ingest:
+        return ingest_main(args)
+    if args.pages:
+        return pages_main(args)
 
     import torch
 
+    from flare_amd import _native
     from flare_amd.store import Adam, PooledTableShard, RowWiseAdagrad, Uniform
     from flare_amd.workload import make_workload
 
@@ -336,6 +577,17 @@ def main() -> int:
 
     overlap = args.overlap
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    # markers inside the update call, after sums_kernel and after the folds (recorded once
+    # here so that each event exists before its handle is taken).  The update call launches
+    # nothing before sums_kernel or after apply_kernel, so ev[4] and ev[5] bound those two.
+    # Each record is a marker packet of a few microseconds on the stream, so none is
+    # recorded twice at one point.
+    markers = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for mk in markers:
+        for e in mk:
+            e.record(stream)
+    handles = [(ctypes.c_void_p * 4)(None, mk[0].cuda_event, mk[1].cuda_event, None) for mk in markers]
+    lib = _native.library()
     aux = torch.cuda.Stream(device=device)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
@@ -358,17 +610,24 @@ def main() -> int:
         else:
             p.forward()  # one launch: the pooled gather kernel
             ev[1].record(stream)
-            ev[2].record(stream)
+            ev[2] = ev[1]
             p.dedup()
             ev[3].record(stream)
-        ev[4].record(stream)
+        if overlap:
+            ev[4].record(stream)
+        else:
+            ev[4] = ev[3]
+        _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
         p.apply(grad, grad_out=grad_out, optimizer=none_opt)
         ev[5].record(stream)
     torch.cuda.synchronize()
     wall1 = time.perf_counter()
+    _native.check(lib.flare_set_update_events(None, 0))
 
+    kernel_bytes = [update_kernel_bytes(b.global_keys(), b.dim, s, b.optimizer) for b in batches]
     step_ms, fwd_ms, dedup_ms, apply_ms = [], [], [], []
     step_gbs, fwd_gbs, upd_gbs = [], [], []
+    sums_ms, fold_ms, applyk_ms, sums_gbs, applyk_gbs = [], [], [], [], []
     for i, ev in enumerate(events):
         b = batches[order[i]]
         f = ev[0].elapsed_time(ev[1])
@@ -383,12 +642,32 @@ def main() -> int:
         step_gbs.append((fb + bb) / (t * 1e-3) / 1e9)
         fwd_gbs.append(fb / (f * 1e-3) / 1e9)
         upd_gbs.append(ub / (a * 1e-3) / 1e9)
+        mk = markers[i]
+        sm, fm, am = ev[4].elapsed_time(mk[0]), mk[0].elapsed_time(mk[1]), mk[1].elapsed_time(ev[5])
+        sums_ms.append(sm)
+        fold_ms.append(fm)
+        applyk_ms.append(am)
+        sb, ab = kernel_bytes[order[i]]
+        sums_gbs.append(sb / (sm * 1e-3) / 1e9)
+        applyk_gbs.append(ab / (am * 1e-3) / 1e9)
     med = statistics.median(step_ms)
     rows = w0.batch * w0.num_tables
     achieved_step = statistics.median(step_gbs)
     fb0, bb0, ub0 = step_bytes(w0.num_ids, uniques[0], w0.batch, w0.num_tables, w0.dim, s,
                                w0.weights is not None, w0.optimizer)
-    traffic = pooled_kernel_traffic(config)
+    sb0, ab0 = kernel_bytes[0]
+
+    def roofline(kernel, what, gbs, ms, nbytes):
+        return {"kernel": f"{kernel} ({what})", "bound": "hbm", "achieved": statistics.median(gbs),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": statistics.median(gbs) / PEAK_HBM_GBS,
+                "traffic": kernel_traffic(config, kernel), "algorithmic_bytes_per_launch": nbytes,
+                "kernel_ms": statistics.median(ms)}
+
+    kernels = [roofline("pooled_kernel", "CSR pooled gather, forward; one launch per step", fwd_gbs, fwd_ms, fb0),
+               roofline("sums_kernel", "segment sums of long keys; one launch per step", sums_gbs, sums_ms, sb0),
+               roofline("apply_kernel", "short-key sums and row-wise update; one launch per step",
+                        applyk_gbs, applyk_ms, ab0)]
+    dominant = max(kernels, key=lambda k: k["kernel_ms"])
     result = {
         "metric": METRIC,
         "value": rows / (med * 1e-3),
@@ -420,23 +699,17 @@ def main() -> int:
             "forward_pooled_gather": statistics.median(fwd_ms),
             "dedup_sort_unique": statistics.median(dedup_ms),
             "segment_reduce_update": statistics.median(apply_ms),
+            "update_sums_kernel": statistics.median(sums_ms),
+            "update_folds": statistics.median(fold_ms),
+            "update_apply_kernel": statistics.median(applyk_ms),
         },
         "phases_gbs": {
             "forward_pooled_gather": statistics.median(fwd_gbs),
             "segment_reduce_update": statistics.median(upd_gbs),
         },
         "wall_ms_per_step": (wall1 - wall0) * 1e3 / args.steps,
-        "roofline": {
-            "kernel": "pooled_kernel (CSR pooled gather, forward; one launch per step)",
-            "bound": "hbm",
-            "achieved": statistics.median(fwd_gbs),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": statistics.median(fwd_gbs) / PEAK_HBM_GBS,
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": fb0,
-            "kernel_ms": statistics.median(fwd_ms),
-        },
+        "roofline": dominant,
+        "roofline_kernels": kernels,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -1596,6 +1596,16 @@ int choose_shape(int dim, bool vec4_ok, Shape *out) {
 
 
 
+// Optional timing markers of the calling thread (flare_set_update_events):
+// recorded on the update's stream before sums_kernel, after it, after the
+// folds and after apply_kernel (null entries record nothing).
+thread_local hipEvent_t t_update_events[4] = {};
+thread_local int t_update_event_count = 0;
+
+inline void mark_update(int i, hipStream_t s) {
+  if (i < t_update_event_count && t_update_events[i]) (void)hipEventRecord(t_update_events[i], s);
+}
+
 template <typename Tag, int VEC, int MODE>
 int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
   auto grid = [&](int g) { return static_cast<int>(std::max<int64_t>(1, ceil_div(a.units, 256 / g))); };
@@ -1622,12 +1632,16 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
     return static_cast<int>(std::min<int64_t>(16384, std::max<int64_t>(1, ceil_div(items, 256 / g))));
   };
 #define FLARE_UPDATE_PAIR(G_, NC_)                                                          \
+  mark_update(0, s);                                                                        \
   if (a.grad_bf16) sums_kernel<Tag, VEC, G_, NC_, MODE, true><<<grid(G_), 256, 0, s>>>(a);  \
   else sums_kernel<Tag, VEC, G_, NC_, MODE, false><<<grid(G_), 256, 0, s>>>(a);            \
+  mark_update(1, s);                                                                        \
   fold_chunks_kernel<VEC, G_, NC_><<<chunk_grid(G_), 256, 0, s>>>(a);                       \
   fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
+  mark_update(2, s);                                                                        \
   if (a.grad_bf16) apply_kernel<Tag, VEC, G_, NC_, MODE, true><<<apply_grid(G_), 256, 0, s>>>(a); \
-  else apply_kernel<Tag, VEC, G_, NC_, MODE, false><<<apply_grid(G_), 256, 0, s>>>(a);
+  else apply_kernel<Tag, VEC, G_, NC_, MODE, false><<<apply_grid(G_), 256, 0, s>>>(a);     \
+  mark_update(3, s);
   if (sh.nc == 1) {
     switch (sh.g) {
       case 8: FLARE_UPDATE_PAIR(8, 1) break;
@@ -1868,6 +1882,14 @@ using namespace flare;
 // ----------------------------------------------------------------------------
 // scatter / scatter_pooled
 // ----------------------------------------------------------------------------
+extern "C" int flare_set_update_events(void *const *events, int32_t count) {
+  if (count < 0 || count > 4 || (count > 0 && events == nullptr))
+    return fail(FLARE_ERR_ARGUMENT, "update events: count must be 0..4 with that many events, got %d", count);
+  for (int i = 0; i < count; ++i) t_update_events[i] = static_cast<hipEvent_t>(events[i]);
+  t_update_event_count = count;
+  return FLARE_OK;
+}
+
 extern "C" size_t flare_scatter_workspace_bytes(int64_t slots, int64_t emb_rows, int32_t dim) {
   (void)emb_rows;
   return layout_workspace(nullptr, slots, 4, std::max(dim, 1), false, false, true).total_bytes;

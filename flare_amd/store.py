@@ -400,13 +400,16 @@ class EmbeddingStore:
             steps = torch.zeros(n, dtype=torch.int32, device=dev)
         if values.dtype == torch.bfloat16:
             values = values.to(torch.float32)
+        # device -> host into pinned buffers (about 50 GB/s, against about 4 GB/s for
+        # pageable ones); the page's numpy arrays keep their buffers alive
+        host = [_pinned_copy(t) for t in (keys, values, state, steps)]
         self.stream.synchronize()
         return {
             "embedding_dim": table.dim,
-            "keys": keys.cpu().numpy().view(np.uint64),
-            "values": values.cpu().numpy().reshape(-1),
-            "optimizer_states": state.cpu().numpy().reshape(-1),
-            "steps": steps.cpu().numpy().view(np.uint32),
+            "keys": host[0].numpy().view(np.uint64),
+            "values": host[1].numpy().reshape(-1),
+            "optimizer_states": host[2].numpy().reshape(-1),
+            "steps": host[3].numpy().view(np.uint32),
         }
 
     def _stored(self, dim: int):
@@ -482,6 +485,13 @@ class EmbeddingStore:
 # ----------------------------------------------------------------------------
 # DynamicEmbeddingStore: arbitrary int64 keys through an HBM key -> row map
 # ----------------------------------------------------------------------------
+def _pinned_copy(t: torch.Tensor) -> torch.Tensor:
+    """A pinned host copy of device tensor ``t``, enqueued on the current stream."""
+    h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    h.copy_(t, non_blocking=True)
+    return h
+
+
 def _map_slots(rows: int) -> int:
     """Power-of-two slot count keeping the map at most half full."""
     slots = 64

@@ -208,6 +208,17 @@ int flare_sparse_update_ex(void *table, int32_t value_dtype, int64_t rows,
                            int32_t *nonfinite_out, int32_t normalization_steps,
                            void *workspace, size_t workspace_bytes, void *stream);
 
+/* Timing markers for the calling thread, with no counterpart in the reference
+ * (a profiling hook, as NVTX ranges are for CUDA code): while count (0..4) is
+ * non-zero, every update entry point called from this thread records
+ * events[0] on its stream before the segment sums kernel, events[1] after
+ * it, events[2] after the hot-key folds and events[3] after the apply
+ * kernel; a null entry records nothing at its point (each record is a
+ * marker packet of a few microseconds).  The events are the caller's
+ * (hipEvent_t, created and kept alive by the caller until the work is done);
+ * count 0 turns the markers off. */
+int flare_set_update_events(void *const *events, int32_t count);
+
 /* require_finite_sparse_values (sparse_precision.py:121-148) on the device:
  * *nonfinite_out (device int32) = 1 when any of the count float32 / float16 /
  * bfloat16 elements is inf or NaN, else 0.  Sets device error bit 8 too. */

@@ -132,3 +132,12 @@ def test_gradient_transport_dtype_validation_on_host():
         _native.check(status)
     status = _call("flare_check_finite", None, _native.FLOAT32, -1, None, None)
     assert status == _native.ERR_SHAPE
+
+
+def test_update_event_markers_validation_on_host():
+    assert _call("flare_set_update_events", None, 5) == _native.ERR_ARGUMENT
+    assert "count must be 0..4" in _native.last_error()
+    assert _call("flare_set_update_events", None, 2) == _native.ERR_ARGUMENT
+    nulls = (ctypes.c_void_p * 2)(None, None)  # null entries: no marker at those points
+    assert _call("flare_set_update_events", ctypes.cast(nulls, ctypes.c_void_p), 2) == _native.OK
+    assert _call("flare_set_update_events", None, 0) == _native.OK
