@@ -73,19 +73,23 @@ def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weight
     return fwd, bwd, update
 
 
-def update_kernel_bytes(keys, dim: int, s: int, optimizer: str) -> tuple[int, int]:
-    """Algorithmic HBM bytes of the two update kernels for one batch of global row keys.
+def update_kernel_bytes(w, s: int) -> tuple[int, int]:
+    """Algorithmic HBM bytes of the two update kernels for one batch ``w``.
 
     Keys are stably sorted; a key is "long" when its sorted positions cross a 64-position
     unit boundary or number more than 4 (those are summed by sums_kernel, one partial row per
-    unit piece), else "short" (summed inside apply_kernel).
-    sums_kernel : N_long * (D*4 gradient row + 4 row index) + P_long * D*4 partial rows
-    apply_kernel: U * (2*D*s row read and write + 2*S state) + N_short * (D*4 + 4)
+    unit piece), else "short" (summed inside apply_kernel).  A bag's gradient row is read once
+    per kernel however many of its occurrences that kernel sums (R_long, R_short: distinct
+    bags among the long and the short occurrences).
+    sums_kernel : R_long * D*4 gradient rows + N_long * 4 row indices + P_long * D*4 partials
+    apply_kernel: U * (2*D*s row read and write + 2*S state) + R_short * D*4 + N_short * 4
                   + U_long * D*4 (the long key's folded sum)
     """
     import numpy as np
 
-    _, counts = np.unique(keys, return_counts=True)
+    keys = w.global_keys()
+    dim = w.dim
+    uniq, inverse, counts = np.unique(keys, return_inverse=True, return_counts=True)
     starts = np.cumsum(counts) - counts
     h = starts // 64
     last = (starts + counts - 1) // 64
@@ -94,13 +98,17 @@ def update_kernel_bytes(keys, dim: int, s: int, optimizer: str) -> tuple[int, in
     p_long = int((last - h + 1)[long_].sum())
     u, u_long = int(counts.size), int(long_.sum())
     n_short = int(counts.sum()) - n_long
-    if optimizer == "none":
+    bag = np.repeat(np.arange(w.num_tables * w.batch, dtype=np.int64), np.diff(w.offsets))
+    occ_long = long_[inverse.reshape(-1)]
+    r_long = int(np.unique(bag[occ_long]).size)
+    r_short = int(np.unique(bag[~occ_long]).size)
+    if w.optimizer == "none":
         rows_state = u * dim * 4
     else:
-        state = 2 * dim * 4 + 4 if optimizer == "adam" else STATE_BYTES[optimizer]
+        state = 2 * dim * 4 + 4 if w.optimizer == "adam" else STATE_BYTES[w.optimizer]
         rows_state = 2 * u * dim * s + 2 * u * state
-    sums = n_long * (dim * 4 + 4) + p_long * dim * 4
-    apply = rows_state + n_short * (dim * 4 + 4) + u_long * dim * 4
+    sums = r_long * dim * 4 + n_long * 4 + p_long * dim * 4
+    apply = rows_state + r_short * dim * 4 + n_short * 4 + u_long * dim * 4
     return sums, apply
 
 
@@ -624,7 +632,7 @@ def main() -> int:
     wall1 = time.perf_counter()
     _native.check(lib.flare_set_update_events(None, 0))
 
-    kernel_bytes = [update_kernel_bytes(b.global_keys(), b.dim, s, b.optimizer) for b in batches]
+    kernel_bytes = [update_kernel_bytes(b, s) for b in batches]
     step_ms, fwd_ms, dedup_ms, apply_ms = [], [], [], []
     step_gbs, fwd_gbs, upd_gbs = [], [], []
     sums_ms, fold_ms, applyk_ms, sums_gbs, applyk_gbs = [], [], [], [], []
