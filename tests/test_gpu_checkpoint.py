@@ -116,3 +116,29 @@ def test_assign_sets_rows_and_non_finite_state_is_visible(gpu_device, no_device_
     assert np.isnan(np.asarray(pages[0]["values"])[0])
     assert store.optimizer_enabled() and store.table_dims() == [2] and store.num_slots() == 1
     no_device_errors()
+
+
+def test_exported_pages_own_their_host_memory(gpu_device, no_device_errors):
+    """Page arrays stay valid and unchanged after later exports and after the store is gone."""
+    import gc
+
+    from flare_amd.store import DynamicEmbeddingStore, RowWiseAdagrad
+
+    store = DynamicEmbeddingStore(4096, [8, 24], value_dtype="float32", optimizer=RowWiseAdagrad(lr=0.1), seed=3)
+    rng = np.random.default_rng(9)
+    keys = np.unique(rng.integers(0, 2 ** 40, 3000, dtype=np.int64))
+    for dim in (8, 24):
+        store.lookup_or_insert(keys, dim)
+    first = store.export_page_images(page_keys=700)
+    copies = [{k: (np.array(v, copy=True) if isinstance(v, np.ndarray) else v) for k, v in p.items()} for p in first]
+    store.assign(keys, np.full((keys.size, 8), 2.5, np.float32))
+    second = store.export_page_images(page_keys=700)
+    del store
+    gc.collect()
+    torch.cuda.empty_cache()
+    assert sorted(int(p["embedding_dim"]) for p in first) == sorted(int(p["embedding_dim"]) for p in second)
+    for page, copy in zip(first, copies):
+        for name in ("keys", "values", "optimizer_states", "steps"):
+            np.testing.assert_array_equal(page[name], copy[name])
+    assert any(np.all(np.asarray(p["values"]) == 2.5) for p in second if int(p["embedding_dim"]) == 8)
+    no_device_errors()
