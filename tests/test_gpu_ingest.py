@@ -57,3 +57,20 @@ def test_errors_match_the_reference(gpu_device, no_device_errors):
     with pytest.raises(ValueError, match="exceeds origin length"):
         unique_global_flat_positions([np.asarray([0, 3, 4])], np.asarray([0, 2]), [2], np.asarray([5, 6]), "g")
     no_device_errors(1)
+
+
+def test_empty_first_indices_and_empty_lists(gpu_device, no_device_errors):
+    from flare_amd.ingest import unique_global_flat_positions
+
+    out = unique_global_flat_positions([np.asarray([0, 0, 0], np.int64)], np.zeros(0, np.int64), [4],
+                                       np.asarray([0, 1], np.int64))
+    assert isinstance(out, np.ndarray) and out.dtype == np.int32 and out.size == 0
+    # rows whose lists are all empty around one non-empty row; origins out of order
+    splits = [np.asarray([0, 0, 0, 3, 3], np.int64), np.asarray([0, 2, 2, 5], np.int64)]
+    first = np.asarray([0, 1, 2, 3, 4], np.int64)
+    origin = np.asarray([9, 4, 7, 0], np.int64)
+    expected = O.nested_global_positions(splits, first, [3, 4], origin)
+    got = unique_global_flat_positions(splits, first, [3, 4], origin)
+    np.testing.assert_array_equal(got, expected)
+    assert got.tolist() == [7 * 12 + 0, 7 * 12 + 1, 7 * 12 + 2 * 4 + 0, 7 * 12 + 2 * 4 + 1, 7 * 12 + 2 * 4 + 2]
+    no_device_errors()

@@ -154,3 +154,25 @@ def test_gradient_for_a_key_without_row_is_reported(gpu_device, no_device_errors
     np.testing.assert_allclose(after.cpu().numpy()[0], before.cpu().numpy()[0] - 1.0, rtol=1e-6)
     assert (after.cpu().numpy()[1] == 0).all()
     no_device_errors(1)
+
+
+def test_int64_min_is_not_storable(gpu_device, no_device_errors):
+    """INT64_MIN marks empty slots: it gets no row (row -1, zero values) and sets error bit 1,
+    while the other keys of the call are inserted in first-occurrence order as usual."""
+    from flare_amd.store import DynamicEmbeddingStore, Sgd
+
+    lo = np.iinfo(np.int64).min
+    keys = np.asarray([7, lo, -7, lo, 7, 2 ** 62], np.int64)
+    store = DynamicEmbeddingStore(64, [8], value_dtype="float32", optimizer=Sgd(), seed=5)
+    oracle = O.KeyMap(64)
+    values, _ = store.lookup_or_insert(keys, 8)
+    rows = store.rows(keys, 8)
+    store.synchronize()
+    e_rows, _ = oracle.lookup_or_insert(keys)
+    np.testing.assert_array_equal(rows.cpu().numpy(), e_rows)
+    assert e_rows.tolist() == [0, -1, 1, -1, 0, 2]
+    v = values.cpu().numpy()
+    assert (v[[1, 3]] == 0).all()
+    np.testing.assert_array_equal(v[[0, 2, 5]], O.keymap_initial_values(keys[[0, 2, 5]], 8, -0.01, 0.01, 5, "float32"))
+    assert store.size(8) == 3 and store.contains(np.asarray([lo], np.int64), 8).tolist() == [False]
+    no_device_errors(1)
