@@ -71,14 +71,22 @@ struct PooledArgs {
 // 128 bf16 rows of 128), 8 when rows are stored directly.
 constexpr int kBagsPerGroupStaged = 4;
 constexpr int kBagsPerGroupDirect = 8;
-// Long bags (kLong: at least kLongBagLength ids per bag on average): one bag
-// per lane group and kLongDepth rows in flight, so that the longest bag, not
-// the group's total, sets the chain of row loads.
+// Long bags (kLong: at least kLongBagLength ids per bag on average):
+// kLongDepth rows in flight, and one bag per lane group when groups are wide
+// (G >= 16: at most 4 groups per wave), so that the longest bag, not the
+// group's total, sets the chain of row loads.  Narrow groups (G <= 8: 8 or
+// more per wave) take kLongBagsNarrow bags each, pooled as one run: a wave
+// waits for its slowest group, and over 8 single bags of varied lengths that
+// one is far above the mean (about 2.7x for geometric lengths), while sums of
+// several bags vary less.
 constexpr int64_t kLongBagLength = 8;
 constexpr int kLongDepth = 8;
+constexpr int kLongBagsNarrow = 4;
 
 template <bool kStage, bool kLong>
-constexpr int bags_per_group() { return kLong ? 1 : (kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect); }
+constexpr int bags_per_group(int g) {
+  return kLong ? (g <= 8 ? kLongBagsNarrow : 1) : (kStage ? kBagsPerGroupStaged : kBagsPerGroupDirect);
+}
 
 // Resolve one id to a table row (or -1 for a pad / out-of-range slot).
 template <bool kCsr, typename IdT>
@@ -113,7 +121,7 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // is stored when finished.
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
-  constexpr int kBagsPerGroup = bags_per_group<kStage, kLong>();
+  constexpr int kBagsPerGroup = bags_per_group<kStage, kLong>(G);
   using E = typename Tag::elem;
   using R = RawVec<Tag, VEC>;
   constexpr int kGroups = kThreads / G;
@@ -284,7 +292,7 @@ constexpr int64_t kStageBytes = 32768;
 
 template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 int launch_pooled_gs(const PooledArgs &a, int G, hipStream_t s) {
-  const int64_t per_block = (kThreads / G) * bags_per_group<kStage, kLong>();
+  const int64_t per_block = (kThreads / G) * bags_per_group<kStage, kLong>(G);
   const int grid = grid_for(a.bags, per_block);
   const size_t lds = kStage ? static_cast<size_t>(per_block) * a.dim * sizeof(typename Tag::elem) : 0;
   switch (G) {
@@ -300,7 +308,7 @@ int launch_pooled_gs(const PooledArgs &a, int G, hipStream_t s) {
 
 template <typename Tag, int VEC, int L, bool kCsr, typename IdT, bool kLong>
 int launch_pooled_g(const PooledArgs &a, int G, hipStream_t s) {
-  const int64_t stage = static_cast<int64_t>(kThreads / G) * bags_per_group<true, kLong>() * a.dim *
+  const int64_t stage = static_cast<int64_t>(kThreads / G) * bags_per_group<true, kLong>(G) * a.dim *
                         sizeof(typename Tag::elem);
   if (VEC * sizeof(typename Tag::elem) == 16 && stage <= kStageBytes)
     return launch_pooled_gs<Tag, VEC, L, kCsr, IdT, true, kLong>(a, G, s);
