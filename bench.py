@@ -511,7 +511,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only (the tables of one worker's shard on one MI355X); "
-              f"--gpus {args.gpus} is not supported by this build", file=sys.stderr)
+              f"--gpus {args.gpus} is not supported (one process, one GPU)", file=sys.stderr)
         return 2
 
     if args.keymap:

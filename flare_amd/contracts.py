@@ -18,7 +18,7 @@ import numpy as np
 from flare_amd.precision import require_sparse_gradient_dtype, require_sparse_value_dtype
 
 SparsePooledWidths = tuple[int, ...]
-# The reference's names ("cupy", "cpu_numba", "jax") plus this build's "hip".
+# The reference's names ("cupy", "cpu_numba", "jax") plus this library's "hip".
 SPARSE_EMBEDDING_OPERATOR_BACKENDS = ("hip",)
 
 

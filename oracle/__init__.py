@@ -2,5 +2,5 @@
 
 Nothing in the product imports this package.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it,
-and only as the checker (or, for ``bench.py``, as the timed CPU baseline).
+and only to check results (or, for ``bench.py``, as the timed CPU baseline).
 """

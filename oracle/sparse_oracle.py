@@ -37,7 +37,7 @@ How each part is pinned (tests/test_oracle.py, tests/test_golden.py):
   outputs for seed 1234567; keymap_initial_values by its range, moments and
   independence from the batch.  The initial values themselves have no
   counterpart in the reference (its store's initializer stream is external):
-  parity unpinned against the reference, pinned only as this build's own
+  parity unpinned against the reference, pinned only as this library's own
   definition.
 
 Parity unpinned (only the external sparse_embedding store defines these, and
@@ -702,7 +702,7 @@ def nested_global_positions(nested_splits, first_indices, widths, origin_indices
 # dynamic key -> row map (the dynamic store's lookup_or_insert)
 # The reference drives an external store: lookup_or_insert(keys, dim)
 # (dynamic_embedding.py:397-399) with new rows from Uniform(-0.01, 0.01)
-# (:262-263).  This restates this build's definition of it.
+# (:262-263).  This restates the HIP library's definition of it.
 # --------------------------------------------------------------------------
 _MIX1 = np.uint64(0xBF58476D1CE4E5B9)
 _MIX2 = np.uint64(0x94D049BB133111EB)
