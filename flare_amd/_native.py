@@ -67,6 +67,10 @@ SIGNATURES = {
     "flare_sparse_update_ex": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i64, _vp, _i32, _i32, _vp, _i32, _vp, _sz, _vp]),
     "flare_check_finite": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "flare_set_update_events": (_i32, [_vp, _i32]),
+    "flare_zero_bytes": (_i32, [_vp, _i64, _vp]),
+    "flare_stream_create": (_i32, [_vp]),
+    "flare_stream_synchronize": (_i32, [_vp]),
+    "flare_stream_destroy": (_i32, [_vp]),
     "flare_keymap_bytes": (_sz, [_i64]),
     "flare_keymap_init": (_i32, [_vp, _i64, _vp]),
     "flare_keymap_workspace_bytes": (_sz, [_i64]),

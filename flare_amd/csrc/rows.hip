@@ -1,7 +1,9 @@
-// Row copies between device tables: gather (dst_index NULL), scatter
-// (src_index NULL) or both.  Used by the stores' assign and checkpoint
-// page-image export / import; rows move as raw bytes, so every dtype
-// (storage values, fp32 optimizer state, int32 step counters) shares it.
+// Raw byte movement.  Row copies between device tables: gather (dst_index
+// NULL), scatter (src_index NULL) or both, used by the stores' assign and
+// checkpoint page-image export / import; rows move as raw bytes, so every
+// dtype (storage values, fp32 optimizer state, int32 step counters) shares
+// it.  And a zero fill: a kernel, not hipMemsetAsync, so that a caller may
+// capture it in a HIP graph.
 #include "common.hpp"
 
 #include <algorithm>
@@ -32,10 +34,38 @@ __global__ __launch_bounds__(kThreads) void copy_rows_kernel(const U *__restrict
   }
 }
 
+template <typename U>
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(U *__restrict__ dst, int64_t units) {
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; t < units;
+       t += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[t] = U{};
+}
+
 }  // namespace
 }  // namespace flare
 
 using namespace flare;
+
+extern "C" int flare_zero_bytes(void *dst, int64_t bytes, void *stream) {
+  if (bytes < 0) return fail(FLARE_ERR_SHAPE, "byte count %lld is negative", static_cast<long long>(bytes));
+  if (bytes == 0) return FLARE_OK;
+  if (!dst) return fail(FLARE_ERR_ARGUMENT, "zero fill buffer is null");
+  hipStream_t s = as_stream(stream);
+  int unit = 1;
+  for (int c : {16, 4}) {
+    if (bytes % c == 0 && aligned(dst, c)) {
+      unit = c;
+      break;
+    }
+  }
+  const int64_t units = bytes / unit;
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(units, kThreads), 1 << 16));
+  if (unit == 16) fill_zero_kernel<uint4><<<grid, kThreads, 0, s>>>(static_cast<uint4 *>(dst), units);
+  else if (unit == 4) fill_zero_kernel<uint32_t><<<grid, kThreads, 0, s>>>(static_cast<uint32_t *>(dst), units);
+  else fill_zero_kernel<uint8_t><<<grid, kThreads, 0, s>>>(static_cast<uint8_t *>(dst), units);
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
 
 extern "C" int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_rows, int64_t row_bytes,
                                const int32_t *src_index, const int32_t *dst_index, int64_t n, void *stream) {

@@ -353,6 +353,21 @@ int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_ro
                     int64_t row_bytes, const int32_t *src_index,
                     const int32_t *dst_index, int64_t n, void *stream);
 
+/* dst[0 .. bytes) = 0 on the stream, by a fill kernel (not hipMemsetAsync, so
+ * that a caller may capture it in a HIP graph).  Replaces the CuPy backend's
+ * cudaMemsetAsync (src/flare/kernels/backends/gpu_cupy.py:255-300), which
+ * zeroes the outputs of its atomic scatters (:422-524). */
+int flare_zero_bytes(void *dst, int64_t bytes, void *stream);
+
+/* A non-blocking stream at default priority, as the CuPy backend keeps one
+ * per operator (src/flare/kernels/backends/gpu_cupy.py:253), for hosts with
+ * no HIP runtime binding of their own; synchronize and destroy it with the
+ * two calls after.  Every entry point takes such a stream (or NULL: the
+ * default stream) as its last argument. */
+int flare_stream_create(void **stream_out);
+int flare_stream_synchronize(void *stream);
+int flare_stream_destroy(void *stream);
+
 /* Dense global positions (int32) of the unique ids' first occurrences in a
  * ragged batch: _unique_global_flat_positions
  * (src/flare/runtime/fluxway/workers/sparse_input.py:85-113) on the device.

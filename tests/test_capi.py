@@ -141,3 +141,12 @@ def test_update_event_markers_validation_on_host():
     nulls = (ctypes.c_void_p * 2)(None, None)  # null entries: no marker at those points
     assert _call("flare_set_update_events", ctypes.cast(nulls, ctypes.c_void_p), 2) == _native.OK
     assert _call("flare_set_update_events", None, 0) == _native.OK
+
+
+def test_stream_and_zero_fill_validation_on_host():
+    assert _call("flare_zero_bytes", None, -1, None) == _native.ERR_SHAPE
+    assert _call("flare_zero_bytes", None, 0, None) == _native.OK  # nothing to do, no launch
+    assert _call("flare_zero_bytes", None, 8, None) == _native.ERR_ARGUMENT
+    assert _call("flare_stream_create", None) == _native.ERR_ARGUMENT
+    assert _call("flare_stream_destroy", None) == _native.ERR_ARGUMENT
+    assert "null (default) stream" in _native.last_error()
