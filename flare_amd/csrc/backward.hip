@@ -55,7 +55,8 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_tickets = take(16 * 4);
   const size_t o_meta = take(8 * 4);
   const size_t o_scan_status = take(static_cast<size_t>(2) * w.tiles * 4);
-  const size_t o_head_bits = take(static_cast<size_t>(ceil_div(std::max<int64_t>(n, 1), 32)) * 4);
+  // whole tiles, so first_count_kernel reads 16-byte vectors without a tail
+  const size_t o_head_flag = take(static_cast<size_t>(w.tiles) * kSortTile);
   // per tile: every plan's passes x 2^digit bits (8 x 256 for 64-bit keys, 3 x 1024 at most for 32-bit)
   const size_t status_per_tile = std::max<size_t>(kMaxPasses * 256, 3 * kMaxRadix);
   const size_t o_sort_status = take(status_per_tile * w.sort_tiles * 4);
@@ -97,7 +98,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.sorted_scale = need_aux ? reinterpret_cast<float *>(b + o_ssc) : nullptr;
     w.run_grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_rgr) : nullptr;
     w.run_scale = need_aux ? reinterpret_cast<float *>(b + o_rsc) : nullptr;
-    w.head_bits = reinterpret_cast<uint32_t *>(b + o_head_bits);
+    w.head_flag = reinterpret_cast<uint8_t *>(b + o_head_flag);
     w.head_run = reinterpret_cast<uint32_t *>(b + o_head_run);
     w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
     w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
@@ -641,14 +642,13 @@ __global__ __launch_bounds__(kSortThreads) void head_count_kernel(const K *__res
   }
 }
 
-// First occurrences (bits of head_bits) in each kSortTile tile of occurrences.
-__global__ __launch_bounds__(kSortThreads) void first_count_kernel(const uint32_t *__restrict__ head_bits,
-                                                                  uint32_t n,
+// First occurrences (head_flag bytes, 0 or 1) in each kSortTile tile of
+// occurrences: 16 flags per thread (the flag array holds whole tiles).
+__global__ __launch_bounds__(kSortThreads) void first_count_kernel(const uint8_t *__restrict__ head_flag,
                                                                   uint32_t *__restrict__ counts) {
-  static_assert(kSortTile / 32 <= kSortThreads, "one bitmap word per thread");
-  const uint32_t word = blockIdx.x * (kSortTile / 32) + threadIdx.x;
-  uint32_t c = 0;
-  if (threadIdx.x < kSortTile / 32 && word < (n + 31) / 32) c = __popc(head_bits[word]);
+  static_assert(kSortTile == kSortThreads * 16, "one 16-byte vector of flags per thread");
+  const uint4 f = reinterpret_cast<const uint4 *>(head_flag)[blockIdx.x * kSortThreads + threadIdx.x];
+  uint32_t c = __popc(f.x) + __popc(f.y) + __popc(f.z) + __popc(f.w);
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
   __shared__ uint32_t s_sum[kSortThreads / 64];
@@ -684,7 +684,7 @@ template <typename K>
 __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     const K *__restrict__ sk, const uint32_t *__restrict__ sv, uint32_t n, K sentinel,
     int use_sentinel, uint32_t *__restrict__ run_start, uint32_t *__restrict__ unit_first_run,
-    uint32_t *__restrict__ head_bits, uint32_t *__restrict__ head_run,
+    uint8_t *__restrict__ head_flag, uint32_t *__restrict__ head_run,
     uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix,
     uint32_t *__restrict__ run_key,
     const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     if (o < n) {
       if (head[k]) {
         // first occurrence of the key (the sort is stable): mark it for rank_kernel
-        atomicOr(head_bits + (o >> 5), 1u << (o & 31));
+        head_flag[o] = 1;  // one sorted position per occurrence: no other writer
         head_run[o] = r;
       }
       // per sorted position: the gradient row and scale of its occurrence
@@ -776,7 +776,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
 enum UniqueSource : int { kUniqueNone = 0, kUniqueFromValues = 1, kUniqueFromSorted = 2 };
 
 __global__ __launch_bounds__(kSortThreads) void rank_kernel(
-    const uint32_t *__restrict__ head_bits, const uint32_t *__restrict__ head_run, uint32_t n,
+    const uint8_t *__restrict__ head_flag, const uint32_t *__restrict__ head_run, uint32_t n,
     const uint32_t *__restrict__ first_prefix, uint32_t tiles, uint32_t *__restrict__ run_rank,
     int64_t *__restrict__ first_indices, void *__restrict__ unique_out, int unique_source,
     const void *__restrict__ values, int value_bytes, const uint32_t *__restrict__ run_key,
@@ -789,7 +789,7 @@ __global__ __launch_bounds__(kSortThreads) void rank_kernel(
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     const uint32_t i = base + k * kSortThreads + tid;
-    first[k] = (i < n) && ((head_bits[i >> 5] >> (i & 31)) & 1u);
+    first[k] = (i < n) && head_flag[i] != 0;
   }
   FlagScan fs;
   uint32_t total;
@@ -1757,14 +1757,14 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
   head_count_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(sk, n, sentinel, use_sentinel, head_prefix);
   scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
   runs_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
-      sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_bits, w.head_run,
+      sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_flag, w.head_run,
       w.meta, head_prefix, o.run_key, o.grad_row, o.grad_sorted, o.scale,
       o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
       w.run_grad_row, w.run_scale, w.meta + 3);
-  first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_bits, n, first_prefix);
+  first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_flag, first_prefix);
   scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
   rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
-      w.head_bits, w.head_run, n, first_prefix, w.tiles, w.run_rank, o.first_indices,
+      w.head_flag, w.head_run, n, first_prefix, w.tiles, w.run_rank, o.first_indices,
       o.unique_out, o.unique_source, o.values, o.value_bytes, o.run_key, o.unique_count);
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;

@@ -37,7 +37,7 @@ struct Workspace {
   uint32_t *meta;         // [8]: nvalid, unique count, hot-key count, rejected batch, non-finite gradient
   uint32_t *sort_status;  // [passes][sort_tiles][2^digit bits] (last in the zeroed region)
   uint32_t *scan_status;  // [2][tiles]
-  uint32_t *head_bits;    // [ceil(n/32)] bit o set: occurrence o is its key's first
+  uint8_t *head_flag;     // [tiles * kSortTile] 1 at o: occurrence o is its key's first (else 0)
   size_t zero_bytes;      // whole zeroed region (sort status sized for the widest plan)
   size_t sort_status_offset;
   // not initialized
@@ -49,7 +49,7 @@ struct Workspace {
   float *sorted_scale;        // [n] aux of the occurrence at each sorted position
   uint32_t *run_grad_row;     // [n] sorted_grad_row at each key's first position
   float *run_scale;           // [n] sorted_scale at each key's first position
-  uint32_t *head_run;     // [n] run of each first occurrence (where head_bits is set)
+  uint32_t *head_run;     // [n] run of each first occurrence (where head_flag is set)
   uint32_t *run_start;    // [n + 1]
   uint32_t *run_rank;     // [n]
   uint32_t *run_key;      // [n] key of each run (32-bit sorts)
