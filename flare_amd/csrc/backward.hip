@@ -72,7 +72,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
   const size_t o_aux = need_aux ? take(un * 4) : 0;
   const size_t o_ssc = need_aux ? take(un * 4) : 0;
   const size_t o_rsc = need_aux ? take(un * 4) : 0;
-  const size_t o_head_run = take(un * 4);
+  const size_t o_head_run = take(un * 8);
   const size_t o_rs = take((un + 1) * 4);
   const size_t o_rr = take(un * 4);
   const size_t o_rk = take(un * 4);
@@ -99,7 +99,7 @@ Workspace layout_workspace(void *base, int64_t n, int key_bytes, int dim, bool n
     w.run_grad_row = need_grad_row ? reinterpret_cast<uint32_t *>(b + o_rgr) : nullptr;
     w.run_scale = need_aux ? reinterpret_cast<float *>(b + o_rsc) : nullptr;
     w.head_flag = reinterpret_cast<uint8_t *>(b + o_head_flag);
-    w.head_run = reinterpret_cast<uint32_t *>(b + o_head_run);
+    w.head_run = reinterpret_cast<uint2 *>(b + o_head_run);
     w.run_start = reinterpret_cast<uint32_t *>(b + o_rs);
     w.run_rank = reinterpret_cast<uint32_t *>(b + o_rr);
     w.run_key = reinterpret_cast<uint32_t *>(b + o_rk);
@@ -684,7 +684,7 @@ template <typename K>
 __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     const K *__restrict__ sk, const uint32_t *__restrict__ sv, uint32_t n, K sentinel,
     int use_sentinel, uint32_t *__restrict__ run_start, uint32_t *__restrict__ unit_first_run,
-    uint8_t *__restrict__ head_flag, uint32_t *__restrict__ head_run,
+    uint8_t *__restrict__ head_flag, uint2 *__restrict__ head_run,
     uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix,
     uint32_t *__restrict__ run_key,
     const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
@@ -742,7 +742,9 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
       if (head[k]) {
         // first occurrence of the key (the sort is stable): mark it for rank_kernel
         head_flag[o] = 1;  // one sorted position per occurrence: no other writer
-        head_run[o] = r;
+        // the key travels with the run, so rank_kernel reads it in occurrence
+        // order instead of from run_key at random
+        head_run[o] = make_uint2(r, static_cast<uint32_t>(key[k]));
       }
       // per sorted position: the gradient row and scale of its occurrence
       // (grad_sorted: the sort has already put the rows in sorted order)
@@ -776,11 +778,10 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
 enum UniqueSource : int { kUniqueNone = 0, kUniqueFromValues = 1, kUniqueFromSorted = 2 };
 
 __global__ __launch_bounds__(kSortThreads) void rank_kernel(
-    const uint8_t *__restrict__ head_flag, const uint32_t *__restrict__ head_run, uint32_t n,
+    const uint8_t *__restrict__ head_flag, const uint2 *__restrict__ head_run, uint32_t n,
     const uint32_t *__restrict__ first_prefix, uint32_t tiles, uint32_t *__restrict__ run_rank,
     int64_t *__restrict__ first_indices, void *__restrict__ unique_out, int unique_source,
-    const void *__restrict__ values, int value_bytes, const uint32_t *__restrict__ run_key,
-    int64_t *__restrict__ unique_count) {
+    const void *__restrict__ values, int value_bytes, int64_t *__restrict__ unique_count) {
   __shared__ uint32_t s_cnt[160];
   const int tid = threadIdx.x;
   const uint32_t tile = blockIdx.x;
@@ -801,7 +802,8 @@ __global__ __launch_bounds__(kSortThreads) void rank_kernel(
     if (!first[k]) continue;
     const uint32_t i = base + k * kSortThreads + tid;
     const uint32_t rank = prefix + fs.incl[k] - 1;
-    const uint32_t r = head_run[i];
+    const uint2 hr = head_run[i];
+    const uint32_t r = hr.x;
     if (rank >= n || r >= n) continue;
     run_rank[r] = rank;
     if (first_indices) first_indices[rank] = i;
@@ -811,7 +813,7 @@ __global__ __launch_bounds__(kSortThreads) void rank_kernel(
       else
         static_cast<uint32_t *>(unique_out)[rank] = static_cast<const uint32_t *>(values)[i];
     } else if (unique_source == kUniqueFromSorted) {
-      static_cast<int64_t *>(unique_out)[rank] = static_cast<int64_t>(run_key[r]);
+      static_cast<int64_t *>(unique_out)[rank] = static_cast<int64_t>(hr.y);  // 32-bit row keys
     }
   }
 }
@@ -1765,7 +1767,7 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
   scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
   rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
       w.head_flag, w.head_run, n, first_prefix, w.tiles, w.run_rank, o.first_indices,
-      o.unique_out, o.unique_source, o.values, o.value_bytes, o.run_key, o.unique_count);
+      o.unique_out, o.unique_source, o.values, o.value_bytes, o.unique_count);
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }

@@ -49,7 +49,7 @@ struct Workspace {
   float *sorted_scale;        // [n] aux of the occurrence at each sorted position
   uint32_t *run_grad_row;     // [n] sorted_grad_row at each key's first position
   float *run_scale;           // [n] sorted_scale at each key's first position
-  uint32_t *head_run;     // [n] run of each first occurrence (where head_flag is set)
+  uint2 *head_run;        // [n] {run, low 32 key bits} of each first occurrence (where head_flag is set)
   uint32_t *run_start;    // [n + 1]
   uint32_t *run_rank;     // [n]
   uint32_t *run_key;      // [n] key of each run (32-bit sorts)
