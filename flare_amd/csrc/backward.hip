@@ -642,6 +642,27 @@ __global__ __launch_bounds__(kSortThreads) void head_count_kernel(const K *__res
   }
 }
 
+// Up to this many tiles, runs_kernel and rank_kernel add up the per-tile
+// counts of the tiles before theirs themselves (at most 8 L2-resident loads
+// per thread) instead of waiting for a separate scan launch.
+constexpr uint32_t kFusedPrefixTiles = 2048;
+
+// Sum of counts[0 .. tile) over the block; every thread of the block calls it
+// once, at the same point.
+__device__ __forceinline__ uint32_t block_prefix_of_counts(const uint32_t *__restrict__ counts, uint32_t tile) {
+  __shared__ uint32_t s_part[kSortThreads / 64];
+  uint32_t v = 0;
+  for (uint32_t i = threadIdx.x; i < tile; i += kSortThreads) v += counts[i];
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kSortThreads / 64; ++w) t += s_part[w];
+  return t;
+}
+
 // First occurrences (head_flag bytes, 0 or 1) in each kSortTile tile of
 // occurrences: 16 flags per thread (the flag array holds whole tiles).
 __global__ __launch_bounds__(kSortThreads) void first_count_kernel(const uint8_t *__restrict__ head_flag,
@@ -685,7 +706,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     const K *__restrict__ sk, const uint32_t *__restrict__ sv, uint32_t n, K sentinel,
     int use_sentinel, uint32_t *__restrict__ run_start, uint32_t *__restrict__ unit_first_run,
     uint8_t *__restrict__ head_flag, uint2 *__restrict__ head_run,
-    uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix,
+    uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix, int fused_prefix,
     uint32_t *__restrict__ run_key,
     const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
     uint32_t *__restrict__ sorted_grad_row, float *__restrict__ sorted_scale,
@@ -718,7 +739,8 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
   FlagScan fs;
   uint32_t total;
   tile_flag_scan(head, s_cnt, fs, &total);
-  const uint32_t prefix = head_prefix[tile];  // heads before this tile
+  // heads before this tile: scanned counts, or the raw counts added up here
+  const uint32_t prefix = fused_prefix ? block_prefix_of_counts(head_prefix, tile) : head_prefix[tile];
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
     const uint32_t j = base + k * kSortThreads + tid;
@@ -779,7 +801,7 @@ enum UniqueSource : int { kUniqueNone = 0, kUniqueFromValues = 1, kUniqueFromSor
 
 __global__ __launch_bounds__(kSortThreads) void rank_kernel(
     const uint8_t *__restrict__ head_flag, const uint2 *__restrict__ head_run, uint32_t n,
-    const uint32_t *__restrict__ first_prefix, uint32_t tiles, uint32_t *__restrict__ run_rank,
+    const uint32_t *__restrict__ first_prefix, int fused_prefix, uint32_t tiles, uint32_t *__restrict__ run_rank,
     int64_t *__restrict__ first_indices, void *__restrict__ unique_out, int unique_source,
     const void *__restrict__ values, int value_bytes, int64_t *__restrict__ unique_count) {
   __shared__ uint32_t s_cnt[160];
@@ -795,7 +817,8 @@ __global__ __launch_bounds__(kSortThreads) void rank_kernel(
   FlagScan fs;
   uint32_t total;
   tile_flag_scan(first, s_cnt, fs, &total);
-  const uint32_t prefix = first_prefix[tile];  // first occurrences before this tile
+  // first occurrences before this tile: scanned counts, or the raw counts added up here
+  const uint32_t prefix = fused_prefix ? block_prefix_of_counts(first_prefix, tile) : first_prefix[tile];
   if (tid == 0 && tile == tiles - 1 && unique_count) *unique_count = static_cast<int64_t>(prefix + total);
 #pragma unroll
   for (int k = 0; k < kSortItems; ++k) {
@@ -1756,17 +1779,18 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
                   int use_sentinel, const RunsOutputs &o, hipStream_t s) {
   uint32_t *head_prefix = w.scan_status;
   uint32_t *first_prefix = w.scan_status + w.tiles;
+  const int fused = w.tiles <= kFusedPrefixTiles ? 1 : 0;
   head_count_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(sk, n, sentinel, use_sentinel, head_prefix);
-  scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
+  if (!fused) scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
   runs_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
       sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_flag, w.head_run,
-      w.meta, head_prefix, o.run_key, o.grad_row, o.grad_sorted, o.scale,
+      w.meta, head_prefix, fused, o.run_key, o.grad_row, o.grad_sorted, o.scale,
       o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
       w.run_grad_row, w.run_scale, w.meta + 3);
   first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_flag, first_prefix);
-  scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
+  if (!fused) scan_counts_kernel<<<1, 1024, 0, s>>>(first_prefix, w.tiles);
   rank_kernel<<<w.tiles, kSortThreads, 0, s>>>(
-      w.head_flag, w.head_run, n, first_prefix, w.tiles, w.run_rank, o.first_indices,
+      w.head_flag, w.head_run, n, first_prefix, fused, w.tiles, w.run_rank, o.first_indices,
       o.unique_out, o.unique_source, o.values, o.value_bytes, o.unique_count);
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;

@@ -106,3 +106,26 @@ def test_every_radix_plan(gpu_device, no_device_errors, bits):
     np.testing.assert_array_equal(inverse, ei)
     np.testing.assert_array_equal(first, ef)
     no_device_errors()
+
+
+@pytest.mark.parametrize("dtype,span", [(np.int32, 1 << 22), (np.int64, 1 << 40)])
+def test_more_tiles_than_the_fused_prefix_covers(gpu_device, no_device_errors, dtype, span):
+    """2049 tiles of 4096 occurrences and a ragged tail: the runs and ranks take their tile
+    prefixes from separate scan launches (up to 2048 tiles the kernels add them up
+    themselves).  Expected values restate the reference's GPU branch: np.unique with first
+    indices and inverse, then ranks in first-occurrence order."""
+    from flare_amd.unique import unique_first_occurrence
+
+    rng = np.random.default_rng(77)
+    n = 2049 * 4096 + 123
+    values = rng.integers(0, span, size=n).astype(dtype)
+    values[rng.random(n) < 0.3] = values[0]  # one heavy key
+    u_sorted, first_idx, inv_sorted = np.unique(values, return_index=True, return_inverse=True)
+    order = np.argsort(first_idx, kind="stable")
+    rank_of_sorted = np.empty_like(order)
+    rank_of_sorted[order] = np.arange(order.size)
+    unique, inverse, first = unique_first_occurrence(torch.from_numpy(values).to(gpu_device))
+    np.testing.assert_array_equal(unique.cpu().numpy(), u_sorted[order])
+    np.testing.assert_array_equal(first.cpu().numpy(), first_idx[order])
+    np.testing.assert_array_equal(inverse.cpu().numpy(), rank_of_sorted[inv_sorted.reshape(-1)])
+    no_device_errors()
