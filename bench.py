@@ -413,6 +413,49 @@ def pages_main(args) -> int:
     return 0
 
 
+def row_gather_main(args) -> int:
+    """Random-row gather rate of this GPU, the ceiling of the update's gradient gather.
+
+    ``flare_copy_rows`` gathers the 1.26M rows that sums_kernel reads per step on the default
+    workload (long keys' occurrences) at random from a buffer the size of the fp32 pooled
+    gradient (65536 x 26 rows of 512 bytes, 872 MB) into a dense buffer.  Also 256-byte rows
+    (bf16 table rows) from a 5.9 GB buffer, as the apply kernel reads them.
+    """
+    import torch
+
+    from flare_amd import _native
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    stream = torch.cuda.Stream(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4)
+    cases = [("512-byte rows of an 872 MB buffer (fp32 gradient rows)", 65536 * 26, 512, 1_260_000),
+             ("256-byte rows of a 5.9 GB buffer (bf16 table rows)", 23_100_000, 256, 322_463)]
+    for name, rows, row_bytes, n in cases:
+        with torch.cuda.stream(stream):
+            src = torch.empty(rows * row_bytes // 4, dtype=torch.float32, device=device).uniform_(generator=gen)
+            dst = torch.empty(n * row_bytes // 4, dtype=torch.float32, device=device)
+            index = torch.randint(0, rows, (n,), generator=gen, device=device, dtype=torch.int32)
+
+        def call():
+            _native.call("flare_copy_rows", src.data_ptr(), rows, dst.data_ptr(), n, row_bytes,
+                         index.data_ptr(), None, n, int(stream.cuda_stream))
+
+        ms = _event_ms(stream, call, args.steps, args.warmup)
+        moved = n * (2 * row_bytes + 4)  # row read at random, written densely, index read
+        print(json.dumps({
+            "metric": "random row gather GB/s (flare_copy_rows)", "value": moved / (ms * 1e-3) / 1e9,
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_call": ms,
+            "higher_is_better": True, "dtype": "raw bytes", "data": "synthetic (uniform random row indices)",
+            "config": {"workload": f"{n} {name}"},
+            "read_gbs": n * row_bytes / (ms * 1e-3) / 1e9, "rows_per_s": n / (ms * 1e-3),
+        }), flush=True)
+        del src, dst, index
+        torch.cuda.empty_cache()
+    return 0
+
+
 def keymap_main(args) -> int:
     """Dynamic store: lookup_or_insert of one step's unique keys into a 128-wide bf16 table.
 
@@ -505,6 +548,8 @@ def main() -> int:
                     help="measure the dynamic store's key map (lookup_or_insert) instead of the pooled step")
     ap.add_argument("--ingest", action="store_true",
                     help="measure CSR-native ingest (nested global positions) instead of the pooled step")
+    ap.add_argument("--row-gather", action="store_true",
+                    help="measure this GPU's random-row gather rate (the update's gradient gather ceiling)")
     ap.add_argument("--pages", action="store_true",
                     help="measure checkpoint page image export/import instead of the pooled step")
     args = ap.parse_args()
@@ -520,6 +565,8 @@ def main() -> int:
         return ingest_main(args)
     if args.pages:
         return pages_main(args)
+    if args.row_gather:
+        return row_gather_main(args)
 
     import torch
 
