@@ -1053,8 +1053,29 @@ constexpr int kFoldDepth = 16;
 // widens exactly, so this equals casting first and reducing after).
 template <int VEC, bool kBf16>
 __device__ __forceinline__ void load_grad(const UpdateArgs &a, int64_t offset, float (&out)[VEC]) {
-  if constexpr (kBf16) load_as_f32<TagBF16, VEC>(static_cast<const uint16_t *>(a.grad) + offset, out);
-  else load_f32<VEC>(static_cast<const float *>(a.grad) + offset, out);
+  // Each gradient row is read once per kernel (L2 hit rate about 14%), so the
+  // 16- and 8-byte loads are nontemporal: they stream past L2 instead of
+  // evicting lines others reuse (sums_kernel 173 -> 153 us on 1.26M rows).
+  if constexpr (kBf16 && VEC == 4) {
+    typedef unsigned int U2 __attribute__((ext_vector_type(2)));
+    const U2 raw = __builtin_nontemporal_load(
+        reinterpret_cast<const U2 *>(static_cast<const uint16_t *>(a.grad) + offset));
+    uint16_t tmp[4];
+    __builtin_memcpy(tmp, &raw, sizeof(raw));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = TagBF16::to_f32(tmp[i]);
+  } else if constexpr (kBf16) {
+    load_as_f32<TagBF16, VEC>(static_cast<const uint16_t *>(a.grad) + offset, out);
+  } else if constexpr (VEC == 4) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const F4 raw = __builtin_nontemporal_load(reinterpret_cast<const F4 *>(static_cast<const float *>(a.grad) + offset));
+    out[0] = raw.x;
+    out[1] = raw.y;
+    out[2] = raw.z;
+    out[3] = raw.w;
+  } else {
+    load_f32<VEC>(static_cast<const float *>(a.grad) + offset, out);
+  }
 }
 
 // Gradient rows recorded in the workspace are in range whenever the batch's
