@@ -1051,12 +1051,19 @@ constexpr int kFoldDepth = 16;
 
 // VEC consecutive gradient elements as float32 (a bfloat16 transport gradient
 // widens exactly, so this equals casting first and reducing after).
-template <int VEC, bool kBf16>
+// kGrad: bit 1 bfloat16 gradient, bit 2 streamed.  When each gradient row is
+// read about once (no more occurrences than rows: one id per bag), the 16- and
+// 8-byte loads are nontemporal and stream past L2 instead of evicting lines
+// that others reuse (sums_kernel 173 -> 153 us on 1.26M rows of 512 bytes).
+// With longer bags several occurrences read one bag's row, and L2 hits pay.
+constexpr int kGradBf16 = 1;
+constexpr int kGradStream = 2;
+
+template <int VEC, int kGrad>
 __device__ __forceinline__ void load_grad(const UpdateArgs &a, int64_t offset, float (&out)[VEC]) {
-  // Each gradient row is read once per kernel (L2 hit rate about 14%), so the
-  // 16- and 8-byte loads are nontemporal: they stream past L2 instead of
-  // evicting lines others reuse (sums_kernel 173 -> 153 us on 1.26M rows).
-  if constexpr (kBf16 && VEC == 4) {
+  constexpr bool kBf16 = (kGrad & kGradBf16) != 0;
+  constexpr bool kStream = (kGrad & kGradStream) != 0;
+  if constexpr (kBf16 && kStream && VEC == 4) {
     typedef unsigned int U2 __attribute__((ext_vector_type(2)));
     const U2 raw = __builtin_nontemporal_load(
         reinterpret_cast<const U2 *>(static_cast<const uint16_t *>(a.grad) + offset));
@@ -1066,7 +1073,7 @@ __device__ __forceinline__ void load_grad(const UpdateArgs &a, int64_t offset, f
     for (int i = 0; i < 4; ++i) out[i] = TagBF16::to_f32(tmp[i]);
   } else if constexpr (kBf16) {
     load_as_f32<TagBF16, VEC>(static_cast<const uint16_t *>(a.grad) + offset, out);
-  } else if constexpr (VEC == 4) {
+  } else if constexpr (kStream && VEC == 4) {
     typedef float F4 __attribute__((ext_vector_type(4)));
     const F4 raw = __builtin_nontemporal_load(reinterpret_cast<const F4 *>(static_cast<const float *>(a.grad) + offset));
     out[0] = raw.x;
@@ -1108,7 +1115,7 @@ __device__ __forceinline__ float scaled(const UpdateArgs &a, float x, float sc) 
 // piece of a key that spans units goes to this unit's partial slot (1 = the
 // key's first piece, 0 = a later one) for apply_kernel to fold.  The group
 // also writes the inverse (rank of the key) of every position of the unit.
-template <typename Tag, int VEC, int G, int NC, int MODE, bool kBf16Grad>
+template <typename Tag, int VEC, int G, int NC, int MODE, int kGrad>
 __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   if (a.reject && *a.reject) return;
   constexpr int kGroups = 256 / G;
@@ -1257,7 +1264,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
         if (ok && col < D) {
-          load_grad<VEC, kBf16Grad>(a, gr * D + col, x[t][c]);
+          load_grad<VEC, kGrad>(a, gr * D + col, x[t][c]);
         } else {
 #pragma unroll
           for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
@@ -1301,7 +1308,7 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
 // several units is folded from the unit partials left to right: the first
 // unit's slot 1, then slot 0 of each following unit.  The table row (and
 // Adagrad accumulator) is loaded before the gradient.
-template <typename Tag, int VEC, int G, int NC, int MODE, bool kBf16Grad>
+template <typename Tag, int VEC, int G, int NC, int MODE, int kGrad>
 __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
   if (a.reject && *a.reject) return;
   constexpr int kGroups = 256 / G;
@@ -1366,7 +1373,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
           for (int c = 0; c < NC; ++c) {
             const int col = (c * G + lane) * VEC;
             if (ok && col < D) {
-              load_grad<VEC, kBf16Grad>(a, gr * D + col, x[t][c]);
+              load_grad<VEC, kGrad>(a, gr * D + col, x[t][c]);
             } else {
 #pragma unroll
               for (int v = 0; v < VEC; ++v) x[t][c][v] = 0.0f;
@@ -1677,16 +1684,23 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
     const int64_t items = static_cast<int64_t>(a.units) + a.units / (kInlineSpan + 1) + 1;
     return static_cast<int>(std::min<int64_t>(16384, std::max<int64_t>(1, ceil_div(items, 256 / g))));
   };
+  // gradient rows streamed when each is read about once (see load_grad)
+  const int gm = (a.grad_bf16 ? kGradBf16 : 0) | (a.grad_rows > 0 && a.n <= a.grad_rows ? kGradStream : 0);
+#define FLARE_GRAD_LAUNCH(KERNEL, G_, NC_, GRID)                                              \
+  switch (gm) {                                                                             \
+    case 0: KERNEL<Tag, VEC, G_, NC_, MODE, 0><<<GRID, 256, 0, s>>>(a); break;              \
+    case kGradBf16: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16><<<GRID, 256, 0, s>>>(a); break; \
+    case kGradStream: KERNEL<Tag, VEC, G_, NC_, MODE, kGradStream><<<GRID, 256, 0, s>>>(a); break; \
+    default: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16 | kGradStream><<<GRID, 256, 0, s>>>(a); break; \
+  }
 #define FLARE_UPDATE_PAIR(G_, NC_)                                                          \
   mark_update(0, s);                                                                        \
-  if (a.grad_bf16) sums_kernel<Tag, VEC, G_, NC_, MODE, true><<<grid(G_), 256, 0, s>>>(a);  \
-  else sums_kernel<Tag, VEC, G_, NC_, MODE, false><<<grid(G_), 256, 0, s>>>(a);            \
+  FLARE_GRAD_LAUNCH(sums_kernel, G_, NC_, grid(G_))                                         \
   mark_update(1, s);                                                                        \
   fold_chunks_kernel<VEC, G_, NC_><<<chunk_grid(G_), 256, 0, s>>>(a);                       \
   fold_kernel<Tag, VEC, G_, NC_, MODE><<<fold_grid, 256, fold_lds(G_), s>>>(a, fold_depth(G_)); \
   mark_update(2, s);                                                                        \
-  if (a.grad_bf16) apply_kernel<Tag, VEC, G_, NC_, MODE, true><<<apply_grid(G_), 256, 0, s>>>(a); \
-  else apply_kernel<Tag, VEC, G_, NC_, MODE, false><<<apply_grid(G_), 256, 0, s>>>(a);     \
+  FLARE_GRAD_LAUNCH(apply_kernel, G_, NC_, apply_grid(G_))                                  \
   mark_update(3, s);
   if (sh.nc == 1) {
     switch (sh.g) {
@@ -1703,6 +1717,7 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
     }
   }
 #undef FLARE_UPDATE_PAIR
+#undef FLARE_GRAD_LAUNCH
   FLARE_TRY_HIP(hipGetLastError());
   return FLARE_OK;
 }
