@@ -1684,14 +1684,21 @@ int launch_update_vec(const UpdateArgs &a, const Shape &sh, hipStream_t s) {
     const int64_t items = static_cast<int64_t>(a.units) + a.units / (kInlineSpan + 1) + 1;
     return static_cast<int>(std::min<int64_t>(16384, std::max<int64_t>(1, ceil_div(items, 256 / g))));
   };
-  // gradient rows streamed when each is read about once (see load_grad)
+  // gradient rows streamed when each is read about once (see load_grad); only
+  // 4-wide vectors have streamed loads, so narrower shapes keep two variants
   const int gm = (a.grad_bf16 ? kGradBf16 : 0) | (a.grad_rows > 0 && a.n <= a.grad_rows ? kGradStream : 0);
-#define FLARE_GRAD_LAUNCH(KERNEL, G_, NC_, GRID)                                              \
-  switch (gm) {                                                                             \
-    case 0: KERNEL<Tag, VEC, G_, NC_, MODE, 0><<<GRID, 256, 0, s>>>(a); break;              \
-    case kGradBf16: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16><<<GRID, 256, 0, s>>>(a); break; \
-    case kGradStream: KERNEL<Tag, VEC, G_, NC_, MODE, kGradStream><<<GRID, 256, 0, s>>>(a); break; \
-    default: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16 | kGradStream><<<GRID, 256, 0, s>>>(a); break; \
+#define FLARE_GRAD_LAUNCH(KERNEL, G_, NC_, GRID)                                                  \
+  if constexpr (VEC == 4) {                                                                     \
+    switch (gm) {                                                                               \
+      case 0: KERNEL<Tag, VEC, G_, NC_, MODE, 0><<<GRID, 256, 0, s>>>(a); break;                \
+      case kGradBf16: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16><<<GRID, 256, 0, s>>>(a); break; \
+      case kGradStream: KERNEL<Tag, VEC, G_, NC_, MODE, kGradStream><<<GRID, 256, 0, s>>>(a); break; \
+      default: KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16 | kGradStream><<<GRID, 256, 0, s>>>(a); break; \
+    }                                                                                           \
+  } else if (gm & kGradBf16) {                                                                  \
+    KERNEL<Tag, VEC, G_, NC_, MODE, kGradBf16><<<GRID, 256, 0, s>>>(a);                         \
+  } else {                                                                                      \
+    KERNEL<Tag, VEC, G_, NC_, MODE, 0><<<GRID, 256, 0, s>>>(a);                                 \
   }
 #define FLARE_UPDATE_PAIR(G_, NC_)                                                          \
   mark_update(0, s);                                                                        \
