@@ -1,0 +1,41 @@
+"""Host arithmetic of bench.py's per-kernel algorithmic bytes (CPU only), on hand-counted cases."""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+import bench  # noqa: E402
+
+
+def _workload(keys, offsets, batch, tables, dim, optimizer):
+    keys = np.asarray(keys, np.int64)
+    return SimpleNamespace(global_keys=lambda: keys, offsets=np.asarray(offsets, np.int64), batch=batch,
+                           num_tables=tables, dim=dim, optimizer=optimizer)
+
+
+def test_long_short_and_unit_crossing_keys_one_id_per_bag():
+    # sorted positions: key 0 at 0..59 (60 > 4: long, one piece), key 1 at 60..61 (short),
+    # key 2 at 62..64 (crosses position 64: long, two pieces), key 3 at 65..66 and key 4 at
+    # 67..69 (short).  One id per bag, so every occurrence has its own gradient row.
+    keys = [0] * 60 + [1] * 2 + [2] * 3 + [3] * 2 + [4] * 3
+    keys = np.random.default_rng(3).permutation(np.asarray(keys))  # order of occurrence is irrelevant
+    w = _workload(keys, np.arange(71), 70, 1, 4, "rowwise_adagrad")
+    sums, apply = bench.update_kernel_bytes(w, 2)
+    n_long, p_long, u, u_long, n_short = 63, 3, 5, 2, 7
+    assert sums == n_long * 4 * 4 + n_long * 4 + p_long * 4 * 4
+    rows_state = 2 * u * 4 * 2 + 2 * u * 4
+    assert apply == rows_state + n_short * 4 * 4 + n_short * 4 + u_long * 4 * 4
+
+
+def test_a_bag_row_counts_once_per_kernel():
+    # two bags of three ids: key 5 four times (short), keys 7 and 8 once; every occurrence is
+    # short, so sums reads nothing and apply reads each bag's gradient row once
+    w = _workload([5, 5, 5, 5, 7, 8], [0, 3, 6], 2, 1, 4, "sgd")
+    sums, apply = bench.update_kernel_bytes(w, 4)
+    assert sums == 0
+    assert apply == 2 * 3 * 4 * 4 + 2 * 4 * 4 + 6 * 4
