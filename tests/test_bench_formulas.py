@@ -39,3 +39,19 @@ def test_a_bag_row_counts_once_per_kernel():
     sums, apply = bench.update_kernel_bytes(w, 4)
     assert sums == 0
     assert apply == 2 * 3 * 4 * 4 + 2 * 4 * 4 + 6 * 4
+
+
+def test_step_bytes_follow_the_published_formula():
+    # N ids, U unique rows, batch B, T tables, D, storage bytes s; weighted adds N*4 per phase
+    n, u, b, t, d, s = 1000, 300, 64, 4, 16, 2
+    fwd, bwd, upd = bench.step_bytes(n, u, b, t, d, s, True, "rowwise_adagrad")
+    offsets = t * (b + 1) * 4
+    assert fwd == n * 8 + offsets + n * 4 + u * d * s + b * t * d * s
+    rows_state = 2 * u * d * s + 2 * u * 4
+    assert bwd == n * 8 + offsets + n * 4 + b * t * d * 4 + u * 8 + n * 4 + rows_state
+    assert upd == b * t * d * 4 + rows_state + n * 4
+    # Adam: m and v rows plus a step counter per row; gradient-only: reduced rows out
+    _, bwd_adam, _ = bench.step_bytes(n, u, b, t, d, s, False, "adam")
+    assert bwd_adam == n * 8 + offsets + b * t * d * 4 + u * 8 + n * 4 + 2 * u * d * s + 2 * u * (2 * d * 4 + 4)
+    _, bwd_none, _ = bench.step_bytes(n, u, b, t, d, s, False, "none")
+    assert bwd_none == n * 8 + offsets + b * t * d * 4 + u * 8 + n * 4 + u * d * 4
