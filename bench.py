@@ -542,6 +542,8 @@ def main() -> int:
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="before timing, run a plain device-to-device copy of this many MiB three times "
                          "(a kernel of known traffic, to scale FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--layout", choices=["table_major", "sample_major"], default="table_major",
+                    help="pooled row layout: [T, B, D] (the T per-table outputs one after the other) or [B, T, D]")
     ap.add_argument("--overlap", action="store_true",
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
@@ -585,13 +587,13 @@ def main() -> int:
     optimizer = {"rowwise_adagrad": RowWiseAdagrad(lr=0.01, eps=1e-8), "adam": Adam(lr=0.01),
                  "none": RowWiseAdagrad(lr=0.01, eps=1e-8)}[w0.optimizer]
     shard = PooledTableShard(w0.table_rows, w0.dim, value_dtype=w0.value_dtype, optimizer=optimizer,
-                             initializer=Uniform(-w0.init_range, w0.init_range), seed=1)
+                             initializer=Uniform(-w0.init_range, w0.init_range), seed=1, layout=args.layout)
     plans = [shard.plan_step(b.ids, b.offsets, b.batch, pooling=b.pooling, per_sample_weights=b.weights)
              for b in batches]
     gen = torch.Generator(device=device)
     gen.manual_seed(2)
     with torch.cuda.stream(shard.stream):
-        grad = torch.randn((w0.batch, w0.num_tables, w0.dim), generator=gen, device=device,
+        grad = torch.randn(shard.pooled_shape(w0.batch), generator=gen, device=device,
                            dtype=torch.float32).mul_(1e-3)
         grad_out = None
         none_opt = None
@@ -746,6 +748,7 @@ def main() -> int:
             "unique_per_step": uniques[0],
             "rotated_batches": len(plans),
             "dedup": "concurrent with the forward" if overlap else "after the forward, same stream",
+            "pooled_layout": "[T, B, D]" if args.layout == "table_major" else "[B, T, D]",
         },
         "hbm_gbs": achieved_step,
         "hbm_frac": achieved_step / PEAK_HBM_GBS,

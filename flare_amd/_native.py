@@ -20,6 +20,8 @@ OK, ERR_DTYPE, ERR_SHAPE, ERR_WIDTH, ERR_ARGUMENT, ERR_WORKSPACE, ERR_HIP, ERR_L
 FLOAT32, FLOAT16, BFLOAT16, INT32, INT64, UINT32, UINT64 = range(7)
 # flare_pooling
 POOL_SUM, POOL_MEAN, POOL_WEIGHTED = range(3)
+# flare_layout
+LAYOUT_SAMPLE_MAJOR, LAYOUT_TABLE_MAJOR = range(2)
 # flare_optimizer_kind
 OPT_NONE, OPT_SGD, OPT_ADAM, OPT_ROWWISE_ADAGRAD = range(4)
 
@@ -51,7 +53,7 @@ SIGNATURES = {
     "flare_abi_version": (_i32, []),
     "flare_gather": (_i32, [_vp, _i32, _i64, _i32, _vp, _i64, _i32, _vp, _vp]),
     "flare_gather_pooled": (_i32, [_vp, _i32, _i64, _i32, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
-    "flare_gather_pooled_csr": (_i32, [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _vp, _vp]),
+    "flare_gather_pooled_csr": (_i32, [_vp, _i32, _i64, _i32, _vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i32, _vp, _vp, _vp]),
     "flare_scatter_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "flare_scatter": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "flare_scatter_pooled": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -60,8 +62,8 @@ SIGNATURES = {
     "flare_sparse_update_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "flare_sparse_update": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
     "flare_pooled_backward_workspace_bytes": (_sz, [_i64, _i64, _i32]),
-    "flare_pooled_backward": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "flare_pooled_dedup": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_pooled_backward": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_pooled_dedup": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "flare_pooled_apply": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _i64, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "flare_pooled_apply_ex": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _i64, _i32, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "flare_sparse_update_ex": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i64, _vp, _i32, _i32, _vp, _i32, _vp, _sz, _vp]),

@@ -284,8 +284,9 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
 
 // Keys from CSR bags (table-major, bag k = t*batch + b).  The block's bag
 // boundaries are staged in LDS; each occurrence finds its bag by binary
-// search there.  Also writes the gradient row (b*T + t) and, for mean
-// pooling, the bag length of every occurrence.
+// search there.  Also writes the gradient row (b*T + t for [B, T, D] pooled
+// gradients, the bag k itself for [T, B, D]) and, for mean pooling, the bag
+// length of every occurrence.
 constexpr int kPrepMaxBags = 4096;
 
 // Bags per prepare block: about 512 blocks (fewer histogram flushes), at most kPrepMaxBags bags each.
@@ -304,7 +305,8 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
-    float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int per_bag, int *err) {
+    float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int per_bag,
+    int table_major, int *err) {
   __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
@@ -343,7 +345,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
       record_error(err, kErrIndexOutOfRange);
     }
     keys[i] = k;
-    grad_row[i] = static_cast<uint32_t>(b * num_tables + t);
+    grad_row[i] = static_cast<uint32_t>(table_major ? bag : b * num_tables + t);
     if (aux) aux[i] = static_cast<float>(s_off[lo + 1] - s_off[lo]);
     add_histograms(s_hist, k, passes, digit);
   };
@@ -2224,18 +2226,26 @@ int check_pooled_args(int64_t rows, int32_t dim, int32_t num_tables, int64_t bat
     return fail(FLARE_ERR_ARGUMENT, "weighted pooling requires per-sample weights");
   return FLARE_OK;
 }
+
+int check_layout(int32_t layout) {
+  if (layout != FLARE_LAYOUT_SAMPLE_MAJOR && layout != FLARE_LAYOUT_TABLE_MAJOR)
+    return fail(FLARE_ERR_ARGUMENT, "unknown pooled row layout %d", layout);
+  return FLARE_OK;
+}
 }  // namespace
 }  // namespace flare
 
 extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
                                   const int64_t *offsets, int32_t num_tables, int64_t batch,
                                   const int64_t *row_base, int64_t rows, int32_t dim,
-                                  int32_t pooling, int64_t *unique_out,
+                                  int32_t pooling, int32_t layout, int64_t *unique_out,
                                   int64_t *first_indices_out, int64_t *unique_count,
                                   void *workspace, size_t workspace_bytes, void *stream) {
   if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
     return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
   FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, nullptr, false));
+  FLARE_TRY(check_layout(layout));
+  const int table_major = layout == FLARE_LAYOUT_TABLE_MAJOR ? 1 : 0;
   hipStream_t s = as_stream(stream);
   const int64_t bags = batch * num_tables;
   if (n == 0 || bags == 0) {
@@ -2258,11 +2268,13 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
+        table_major, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
-        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag, err);
+        plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
+        table_major, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   return dedup_rows(w, plan, sentinel, err, s, &sorted, first_indices_out, unique_out,
@@ -2368,7 +2380,7 @@ extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t r
                                      const flare_optimizer *optimizer, const void *ids,
                                      int32_t id_dtype, int64_t n, const int64_t *offsets,
                                      int32_t num_tables, int64_t batch, const int64_t *row_base,
-                                     int32_t pooling, const float *weights,
+                                     int32_t pooling, int32_t layout, const float *weights,
                                      const float *pooled_grad, int32_t normalization_steps,
                                      float *grad_out, int64_t *unique_out, int32_t *inverse_out,
                                      int64_t *first_indices_out, int64_t *unique_count,
@@ -2382,8 +2394,9 @@ extern "C" int flare_pooled_backward(void *table, int32_t value_dtype, int64_t r
   FLARE_TRY(optimizer_mode(optimizer, &mode));
   if (mode == kModeUnique && !grad_out) return fail(FLARE_ERR_ARGUMENT, "FLARE_OPT_NONE requires grad_out");
   FLARE_TRY(check_state(mode, state0, state1, step));
+  FLARE_TRY(check_layout(layout));
   FLARE_TRY(flare_pooled_dedup(ids, id_dtype, n, offsets, num_tables, batch, row_base, rows, dim,
-                               pooling, unique_out, first_indices_out, unique_count, workspace,
+                               pooling, layout, unique_out, first_indices_out, unique_count, workspace,
                                workspace_bytes, stream));
   return flare_pooled_apply(table, value_dtype, rows, dim, state0, state1, step, optimizer, n,
                             num_tables, batch, pooling, weights, pooled_grad, normalization_steps,

@@ -61,11 +61,24 @@ struct PooledArgs {
   int32_t max_elements;
   int32_t pad_index;
   int32_t pooling;
+  int32_t table_major;  // CSR: output row o is bag o ([T, B, D]) instead of b*T + t
   const float *weights;
   void *out;
   int64_t bags;
   int *err;
 };
+
+// Blocks are dispatched round-robin over the 8 XCDs of the chip, each with its
+// own L2.  With table-major rows this gives XCD x the x-th contiguous eighth of
+// the bags (so of the tables): a row used by several bags of a table is
+// fetched into one or two L2s instead of all eight, and every block still
+// writes one contiguous range.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_block(int64_t i, int64_t blocks) {
+  const int64_t per = blocks / kXcds, rem = blocks % kXcds;
+  const int64_t x = i % kXcds, j = i / kXcds;
+  return x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+}
 
 // Bags per lane group: 4 when the block stages its rows in LDS (32 KiB for
 // 128 bf16 rows of 128), 8 when rows are stored directly.
@@ -94,7 +107,9 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
                                                int64_t row_hi) {
   const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
   if constexpr (kCsr) {
-    if (id >= 0 && id < row_hi - row_lo) return row_lo + id;
+    // inside the table's own range and inside the whole table (a row_base
+    // whose entries run past table_rows must not read beyond it)
+    if (id >= 0 && id < row_hi - row_lo && row_lo >= 0 && row_lo + id < a.table_rows) return row_lo + id;
     record_error(a.err, kErrIndexOutOfRange);
     return -1;
   } else {
@@ -134,15 +149,22 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
 
   const int lane = threadIdx.x % G;
   const int group = threadIdx.x / G;
-  const int64_t o0 = static_cast<int64_t>(blockIdx.x) * kBagsPerBlock;
+  const int64_t block = (kCsr && a.table_major) ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int64_t o0 = block * kBagsPerBlock;
   const int64_t nout = (a.bags - o0) < kBagsPerBlock ? (a.bags - o0) : kBagsPerBlock;
 
   for (int i = threadIdx.x; i < nout; i += kThreads) {
     const int64_t o = o0 + i;
     if constexpr (kCsr) {
-      const int64_t b = o / a.num_tables;
-      const int64_t t = o - b * a.num_tables;
-      const int64_t bag = t * a.batch + b;
+      int64_t t, bag;
+      if (a.table_major) {
+        t = o / a.batch;
+        bag = o;
+      } else {
+        const int64_t b = o / a.num_tables;
+        t = o - b * a.num_tables;
+        bag = t * a.batch + b;
+      }
       int64_t lo = a.offsets[bag];
       int64_t hi = a.offsets[bag + 1];
       // offsets must start at 0, end at num_ids and never decrease
@@ -427,7 +449,8 @@ extern "C" int flare_gather_pooled_csr(const void *table, int32_t value_dtype, i
                                        int32_t dim, const void *ids, int32_t id_dtype, int64_t n,
                                        const int64_t *offsets, int32_t num_tables, int64_t batch,
                                        const int64_t *row_base, int32_t pooling,
-                                       const float *weights, void *out, void *stream) {
+                                       int32_t layout, const float *weights, void *out,
+                                       void *stream) {
   if (storage_bytes(value_dtype) == 0)
     return fail(FLARE_ERR_DTYPE, "sparse pooled gather requires float16, bfloat16 or float32 embeddings, got dtype code %d", value_dtype);
   if (id_dtype != FLARE_INT32 && id_dtype != FLARE_INT64)
@@ -435,12 +458,15 @@ extern "C" int flare_gather_pooled_csr(const void *table, int32_t value_dtype, i
   if (num_tables <= 0 || batch < 0 || dim <= 0 || table_rows < 0 || n < 0)
     return fail(FLARE_ERR_SHAPE, "invalid CSR pooled gather sizes");
   FLARE_TRY(check_pooling(pooling, weights));
+  if (layout != FLARE_LAYOUT_SAMPLE_MAJOR && layout != FLARE_LAYOUT_TABLE_MAJOR)
+    return fail(FLARE_ERR_ARGUMENT, "unknown pooled row layout %d", layout);
   const int64_t bags = batch * num_tables;
   if (bags == 0) return FLARE_OK;
   int st = FLARE_OK;
   int *err = device_error_word(&st);
   if (!err) return st;
   PooledArgs a{};
+  a.table_major = layout == FLARE_LAYOUT_TABLE_MAJOR ? 1 : 0;
   a.table = table;
   a.table_rows = table_rows;
   a.dim = dim;

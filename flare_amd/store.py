@@ -32,6 +32,7 @@ from flare_amd.conversion import TORCH_VALUE_DTYPES, contiguous, storage_code, t
 from flare_amd.precision import require_sparse_value_dtype
 
 _POOLING = {"sum": _native.POOL_SUM, "mean": _native.POOL_MEAN, "weighted": _native.POOL_WEIGHTED}
+_LAYOUTS = {"sample_major": _native.LAYOUT_SAMPLE_MAJOR, "table_major": _native.LAYOUT_TABLE_MAJOR}
 
 # Gradient transport dtypes read as they are (SPARSE_GRADIENT_TRANSPORT_DTYPES,
 # sparse_precision.py:12-14): bfloat16 widens to float32 on load, exactly.
@@ -649,15 +650,23 @@ class PooledTableShard:
 
     Bags are given in CSR form, table-major: for table ``t`` and sample ``b``
     the bag is ``ids[offsets[t*B + b] : offsets[t*B + b + 1]]`` with
-    table-local row ids.
+    table-local row ids.  Pooled rows (forward output and pooled gradient) are
+    ``[B, T, D]`` with ``layout="sample_major"`` (one group of T features, as
+    ``gather_pooled`` returns it for target widths ``(T, M)``) or ``[T, B, D]``
+    with ``layout="table_major"`` (T single-feature groups, the ``[B, 1, D]``
+    outputs of T ``gather_pooled`` calls one after the other).
     """
 
     def __init__(self, table_rows: Sequence[int], dim: int, *, value_dtype: str = "bfloat16",
                  optimizer: Any = None, initializer: Any = None, seed: int = 0,
-                 device: Any = None):
+                 device: Any = None, layout: str = "sample_major"):
         if not torch.cuda.is_available():
             raise RuntimeError("PooledTableShard requires a ROCm GPU")
+        if layout not in _LAYOUTS:
+            raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
         _native.library()
+        self.layout = layout
+        self._layout_code = _LAYOUTS[layout]
         self.device = _device_of(device)
         self.table_rows = [int(r) for r in table_rows]
         self.num_tables = len(self.table_rows)
@@ -678,6 +687,12 @@ class PooledTableShard:
     @property
     def table(self) -> torch.Tensor:
         return self.state.table
+
+    def pooled_shape(self, batch_size: int) -> tuple[int, int, int]:
+        """Shape of the pooled rows (and pooled gradient) of a batch in this shard's layout."""
+        if self.layout == "table_major":
+            return (self.num_tables, int(batch_size), self.dim)
+        return (int(batch_size), self.num_tables, self.dim)
 
     def _csr(self, ids: Any, offsets: Any, batch_size: int):
         ids_t = contiguous(to_device(ids, self.device).reshape(-1))
@@ -705,21 +720,20 @@ class PooledTableShard:
 
     def lookup_pooled(self, ids: Any, offsets: Any, batch_size: int, *, pooling: str = "sum",
                       per_sample_weights: Any = None, out: torch.Tensor | None = None) -> torch.Tensor:
-        """Forward: ``[B, T, D]`` pooled rows in the storage dtype."""
+        """Forward: pooled rows in the storage dtype, ``pooled_shape(batch_size)``."""
         with torch.cuda.stream(self.stream):
             ids_t, off = self._csr(ids, offsets, batch_size)
             w = self._weights(pooling, per_sample_weights, ids_t.numel())
             if out is None:
-                out = torch.empty((batch_size, self.num_tables, self.dim),
-                                  dtype=self.state.table.dtype, device=self.device)
+                out = torch.empty(self.pooled_shape(batch_size), dtype=self.state.table.dtype,
+                                  device=self.device)
             _native.call(
                 "flare_gather_pooled_csr", self.state.table.data_ptr(),
                 storage_code(self.state.table.dtype), self.total_rows, self.dim,
                 ids_t.data_ptr(), _native.INT32 if ids_t.dtype == torch.int32 else _native.INT64,
                 ids_t.numel(), off.data_ptr(), self.num_tables, batch_size,
-                self.row_base.data_ptr(), _POOLING[pooling], None if w is None else w.data_ptr(),
-                out.data_ptr(),
-                int(self.stream.cuda_stream),
+                self.row_base.data_ptr(), _POOLING[pooling], self._layout_code,
+                None if w is None else w.data_ptr(), out.data_ptr(), int(self.stream.cuda_stream),
             )
         return out
 
@@ -733,7 +747,8 @@ class PooledTableShard:
             w = self._weights(pooling, per_sample_weights, n)
             g = _transport_grad(to_device(pooled_grad, self.device))
             if g.numel() != batch_size * self.num_tables * self.dim:
-                raise ValueError("pooled gradient must be [batch, num_tables, dim]")
+                raise ValueError(f"pooled gradient must be {list(self.pooled_shape(batch_size))} "
+                                 f"({self.layout} layout)")
             opt = optimizer_override if optimizer_override is not None else self.state.native_optimizer
             grad_out = None
             if opt.kind == _native.OPT_NONE:
@@ -756,8 +771,8 @@ class PooledTableShard:
                     "flare_pooled_backward", self.state.table.data_ptr(),
                     storage_code(self.state.table.dtype), self.total_rows, self.dim, s0, s1, st,
                     ctypes.byref(opt), ids_t.data_ptr(), id_code, n, off.data_ptr(),
-                    self.num_tables, batch_size, self.row_base.data_ptr(), _POOLING[pooling], p(w),
-                    g.data_ptr(), int(normalization_steps), p(grad_out), p(unique), p(inverse),
+                    self.num_tables, batch_size, self.row_base.data_ptr(), _POOLING[pooling], self._layout_code,
+                    p(w), g.data_ptr(), int(normalization_steps), p(grad_out), p(unique), p(inverse),
                     p(first), p(count), ws.data_ptr(), nbytes, stream,
                 )
             else:
@@ -781,7 +796,8 @@ class PooledTableShard:
         stream = int(self.stream.cuda_stream)
         _native.call(
             "flare_pooled_dedup", ids_t.data_ptr(), id_code, n, off.data_ptr(), self.num_tables, batch_size,
-            self.row_base.data_ptr(), self.total_rows, self.dim, _POOLING[pooling], p(unique), p(first),
+            self.row_base.data_ptr(), self.total_rows, self.dim, _POOLING[pooling], self._layout_code, p(unique),
+            p(first),
             p(count), ws.data_ptr(), nbytes, stream,
         )
         _native.call(
@@ -843,8 +859,7 @@ class PooledStepPlan:
             self.ids, self.offsets = shard._csr(ids, offsets, self.batch)
             self.n = int(self.ids.numel())
             self.weights = shard._weights(pooling, per_sample_weights, self.n)
-            self.pooled = torch.empty((self.batch, shard.num_tables, shard.dim),
-                                      dtype=shard.state.table.dtype, device=dev)
+            self.pooled = torch.empty(shard.pooled_shape(self.batch), dtype=shard.state.table.dtype, device=dev)
             m = max(self.n, 1)
             self.unique = torch.empty(m, dtype=torch.int64, device=dev)
             self.first_indices = torch.empty(m, dtype=torch.int64, device=dev)
@@ -886,7 +901,7 @@ class PooledStepPlan:
         _native.call(
             "flare_gather_pooled_csr", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
             s.total_rows, s.dim, self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
-            s.num_tables, self.batch, s.row_base.data_ptr(), _POOLING[self.pooling],
+            s.num_tables, self.batch, s.row_base.data_ptr(), _POOLING[self.pooling], s._layout_code,
             None if self.weights is None else self.weights.data_ptr(), self.pooled.data_ptr(),
             self._stream,
         )
@@ -900,7 +915,7 @@ class PooledStepPlan:
         _native.call(
             "flare_pooled_dedup", self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
             s.num_tables, self.batch, s.row_base.data_ptr(), s.total_rows, s.dim,
-            _POOLING[self.pooling], self.unique.data_ptr(), self.first_indices.data_ptr(),
+            _POOLING[self.pooling], s._layout_code, self.unique.data_ptr(), self.first_indices.data_ptr(),
             self.unique_count.data_ptr(), self.workspace.data_ptr(), self.workspace_bytes, stream,
         )
 
@@ -913,8 +928,8 @@ class PooledStepPlan:
         s = self.shard
         if pooled_grad.dtype not in _GRAD_TRANSPORT or not pooled_grad.is_contiguous() or \
                 pooled_grad.numel() != self.batch * s.num_tables * s.dim or pooled_grad.device != s.device:
-            raise ValueError("pooled_grad must be a contiguous float32 or bfloat16 [batch, num_tables, dim] "
-                             "device tensor")
+            raise ValueError(f"pooled_grad must be a contiguous float32 or bfloat16 {list(s.pooled_shape(self.batch))} "
+                             f"device tensor ({s.layout} layout)")
         opt = s.state.native_optimizer if optimizer is None else optimizer
         s0, s1, st = s.state.pointers()
         _native.call(

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define FLARE_ABI_VERSION 1
+#define FLARE_ABI_VERSION 2
 
 /* Status codes; the Python layer maps them to the reference's exception
  * classes (src/flare/kernels/backends/gpu_cupy.py:351-354,398-401,479-483). */
@@ -50,6 +50,17 @@ typedef enum flare_pooling {
   FLARE_POOL_MEAN = 1,     /* divisor max(#valid,1), jax/layers/embedding.py:124-126 */
   FLARE_POOL_WEIGHTED = 2  /* per-sample weights (no reference counterpart)    */
 } flare_pooling;
+
+/* Order of the pooled rows of a CSR batch over T tables and B samples
+ * (pooled output and pooled gradient alike).  SAMPLE_MAJOR is one group of T
+ * features, [B, T, D] as gather_pooled returns it for target widths (T, M)
+ * (contracts.py:63-73).  TABLE_MAJOR packs the T single-feature groups that
+ * T separate gather_pooled calls would return, [B, 1, D] each, one after the
+ * other: [T, B, D], row t*B + b, the bag order of the CSR batch itself. */
+typedef enum flare_layout {
+  FLARE_LAYOUT_SAMPLE_MAJOR = 0,
+  FLARE_LAYOUT_TABLE_MAJOR = 1
+} flare_layout;
 
 typedef enum flare_optimizer_kind {
   FLARE_OPT_NONE = 0,            /* write the deduplicated gradient sum only */
@@ -112,13 +123,15 @@ int flare_gather_pooled(const void *emb, int32_t value_dtype, int64_t emb_rows,
  * row_base[num_tables] == table_rows; ids outside [0, row_base[t+1] -
  * row_base[t]) contribute nothing.  n = number of ids; offsets are clamped
  * to [0, n] (offsets must start at 0, end at n and not decrease; a violation
- * sets the device error word).  out: [batch, num_tables, dim]. */
+ * sets the device error word).  out: [batch, num_tables, dim] for
+ * FLARE_LAYOUT_SAMPLE_MAJOR, [num_tables, batch, dim] for _TABLE_MAJOR. */
 int flare_gather_pooled_csr(const void *table, int32_t value_dtype,
                             int64_t table_rows, int32_t dim, const void *ids,
                             int32_t id_dtype, int64_t n, const int64_t *offsets,
                             int32_t num_tables, int64_t batch,
                             const int64_t *row_base, int32_t pooling,
-                            const float *weights, void *out, void *stream);
+                            int32_t layout, const float *weights, void *out,
+                            void *stream);
 
 /* ---------------------------------------------------------------------------
  * Deduplication and gradient reduction (backward).  These need a device
@@ -234,7 +247,8 @@ size_t flare_pooled_backward_workspace_bytes(int64_t n, int64_t rows,
  * (pooled_grad[b,t,:], times weights[i] for WEIGHTED or / bag length for
  * MEAN), deterministic segment reduction, then the optimizer update of the
  * table rows -- scatter_pooled (gpu_cupy.py:460-524) + accumulate_gradients +
- * optimizer_step fused.  pooled_grad: float32 [batch, num_tables, dim].
+ * optimizer_step fused.  pooled_grad: float32 [batch, num_tables, dim]
+ * (SAMPLE_MAJOR) or [num_tables, batch, dim] (TABLE_MAJOR), as `layout` says.
  * With optimizer->kind == FLARE_OPT_NONE the reduced gradient is written to
  * grad_out [U, dim] in first-occurrence order and the table is not touched.
  * Optional outputs (NULL to skip): unique_out (int64 global rows, first
@@ -246,7 +260,7 @@ int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows,
                           const void *ids, int32_t id_dtype, int64_t n,
                           const int64_t *offsets, int32_t num_tables,
                           int64_t batch, const int64_t *row_base,
-                          int32_t pooling, const float *weights,
+                          int32_t pooling, int32_t layout, const float *weights,
                           const float *pooled_grad, int32_t normalization_steps,
                           float *grad_out, int64_t *unique_out,
                           int32_t *inverse_out, int64_t *first_indices_out,
@@ -257,12 +271,12 @@ int flare_pooled_backward(void *table, int32_t value_dtype, int64_t rows,
  * flare_pooled_dedup needs only the ids (it can run as soon as the batch is
  * known, e.g. right after the forward), flare_pooled_apply consumes the
  * pooled gradient and the dedup left in the workspace (same n, num_tables,
- * batch, rows, dim and pooling).  unique_out / first_indices_out /
+ * batch, rows, dim and pooling; the layout is the dedup's).  unique_out / first_indices_out /
  * unique_count are written by the dedup, inverse_out by the apply. */
 int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
                        const int64_t *offsets, int32_t num_tables, int64_t batch,
                        const int64_t *row_base, int64_t rows, int32_t dim,
-                       int32_t pooling, int64_t *unique_out,
+                       int32_t pooling, int32_t layout, int64_t *unique_out,
                        int64_t *first_indices_out, int64_t *unique_count,
                        void *workspace, size_t workspace_bytes, void *stream);
 

@@ -357,3 +357,73 @@ def test_pooled_step_with_a_key_past_the_fold_chunk(gpu_device, no_device_errors
     assert O.storage_ulp_distance(shard.table.cpu().numpy(), e_table, "float32").max() <= 1
     np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["acc"], rtol=1e-5)
     no_device_errors()
+
+
+SHORT_DIMS = {"bfloat16": (64, 128, 256), "float16": (64, 128, 256), "float32": (32, 64, 128)}
+
+
+@pytest.mark.parametrize("layout", ["sample_major", "table_major"])
+@pytest.mark.parametrize("pooling", ["sum", "mean", "weighted"])
+@pytest.mark.parametrize("storage", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("width", [0, 1, 2])
+def test_short_bag_forward_bit_exact(gpu_device, no_device_errors, layout, pooling, storage, width):
+    """Bags of 0-2 ids (at most 2 on average, a few of 3-5), rows of 128, 256 and 512 bytes,
+    int32 and int64 ids, both pooled row layouts: the forward against the oracle."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    dim = SHORT_DIMS[storage][width]
+    rng = np.random.default_rng(7 + width)
+    table_rows, batch = [9, 300, 41], 777
+    lengths = rng.integers(0, 3, size=len(table_rows) * batch)
+    lengths[5::97] = rng.integers(3, 6, size=lengths[5::97].size)
+    lengths[: lengths.size // 8] = np.minimum(lengths[: lengths.size // 8], 1)
+    assert lengths.sum() <= 2 * lengths.size
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    ids = (rng.integers(0, 1 << 30, size=int(offsets[-1])) % np.asarray(table_rows)[bag_table]).astype(np.int64)
+    weights = rng.uniform(0, 1, size=ids.size).astype(np.float32) if pooling == "weighted" else None
+    shard = PooledTableShard(table_rows, dim, value_dtype=storage, initializer=Uniform(-1.0, 1.0), seed=width,
+                             layout=layout)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    pooled = shard.lookup_pooled(ids.astype(np.int32) if width == 1 else ids, offsets, batch, pooling=pooling,
+                                 per_sample_weights=weights)
+    shard.synchronize()
+    expected = O.gather_pooled_csr(_host(shard.table), ids, offsets, row_base, batch, dim, storage=storage,
+                                   pooling=pooling, weights=weights)
+    if layout == "table_major":
+        expected = np.ascontiguousarray(expected.transpose(1, 0, 2))
+    assert tuple(pooled.shape) == shard.pooled_shape(batch)
+    np.testing.assert_array_equal(_host(pooled), expected)
+    no_device_errors()
+
+
+@pytest.mark.parametrize("config", [2, 4])
+def test_table_major_step_matches_sample_major(gpu_device, no_device_errors, config):
+    """The same step in both pooled row layouts: forward rows transposed, dedup identical, and the
+    same table update (the [T, B, D] gradient is the [B, T, D] one transposed)."""
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    w = make_workload(config, batch=1500, row_scale=0.0005)
+    grad = pooled_grad_host(w)
+    results = {}
+    for layout in ("sample_major", "table_major"):
+        from flare_amd.store import PooledTableShard, RowWiseAdagrad, Uniform
+
+        shard = PooledTableShard(w.table_rows, w.dim, value_dtype=w.value_dtype, optimizer=RowWiseAdagrad(),
+                                 initializer=Uniform(-0.01, 0.01), seed=5, layout=layout)
+        g = grad if layout == "sample_major" else np.ascontiguousarray(grad.transpose(1, 0, 2))
+        plan = shard.plan_step(w.ids, w.offsets, w.batch)
+        pooled = plan.forward()
+        plan.dedup()
+        plan.apply(torch.from_numpy(g).to(gpu_device))
+        shard.synchronize()
+        u = int(plan.unique_count.item())
+        results[layout] = (_host(pooled), plan.unique[:u].cpu().numpy(), plan.inverse[:w.num_ids].cpu().numpy(),
+                           plan.first_indices[:u].cpu().numpy(), _host(shard.table),
+                           shard.state.state0.cpu().numpy())
+    a, b = results["sample_major"], results["table_major"]
+    np.testing.assert_array_equal(a[0].transpose(1, 0, 2), b[0])
+    for x, y in zip(a[1:], b[1:]):
+        np.testing.assert_array_equal(x, y)
+    no_device_errors()
