@@ -70,6 +70,7 @@ SIGNATURES = {
     "flare_check_finite": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "flare_set_update_events": (_i32, [_vp, _i32]),
     "flare_zero_bytes": (_i32, [_vp, _i64, _vp]),
+    "flare_convert": (_i32, [_vp, _i32, _vp, _i32, _i64, _vp]),
     "flare_stream_create": (_i32, [_vp]),
     "flare_stream_synchronize": (_i32, [_vp]),
     "flare_stream_destroy": (_i32, [_vp]),

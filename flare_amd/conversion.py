@@ -1,4 +1,4 @@
-"""Buffer exchange for the HIP path: DLPack in, torch tensors (DLPack producers) out.
+"""Buffer exchange for the HIP path: DLPack (producers or capsules) in, device arrays out.
 
 Device arrays are imported zero-copy (``torch.from_dlpack``); host arrays are
 copied to the device on the operator's stream.  This mirrors
@@ -46,16 +46,32 @@ def dtype_name(dtype: torch.dtype) -> str:
     return str(dtype).replace("torch.", "")
 
 
+def is_dlpack_capsule(value: Any) -> bool:
+    """A legacy DLPack ``PyCapsule`` (named "dltensor"), as ``to_dlpack`` and the
+    reference's ``prepare_dlpack_input`` produce (``dynamic_embedding.py:396-400,514``)."""
+    return type(value).__name__ == "PyCapsule"
+
+
 def to_device(value: Any, device: torch.device, *, non_blocking: bool = True) -> torch.Tensor:
     """Import ``value`` as a torch tensor on ``device`` (caller enters the stream).
 
-    Accepts torch tensors, DLPack producers (device types 1, 2 and 10) and
-    numpy arrays / array-likes.  Raises ``TypeError`` for anything else.
+    Accepts torch tensors, ``DeviceArray``s, DLPack producers (device types 1,
+    2 and 10), legacy DLPack capsules (consumed: a capsule imports once),
+    objects exposing ``__cuda_array_interface__``, and numpy arrays /
+    array-likes.  Raises ``TypeError`` for anything else.
     """
+    from flare_amd.array import DeviceArray
+
     if isinstance(value, torch.Tensor):
         tensor = value
+    elif isinstance(value, DeviceArray):
+        tensor = value.tensor
     elif isinstance(value, np.ndarray):
         tensor = torch.from_numpy(np.ascontiguousarray(value))
+    elif is_dlpack_capsule(value):
+        tensor = torch.from_dlpack(value)
+    elif hasattr(value, "__cuda_array_interface__") and not hasattr(value, "__dlpack__"):
+        tensor = torch.as_tensor(value, device=device)
     elif hasattr(value, "__dlpack__"):
         if not hasattr(value, "__dlpack_device__"):
             raise TypeError(

@@ -41,10 +41,59 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(U *__restrict__ dst
     dst[t] = U{};
 }
 
+// dst[i] = src[i] converted through float32 (exact widening, round-to-nearest-
+// even narrowing); four elements per thread.
+template <typename SrcTag, typename DstTag>
+__global__ __launch_bounds__(kThreads) void convert_kernel(const typename SrcTag::elem *__restrict__ src,
+                                                           typename DstTag::elem *__restrict__ dst, int64_t count) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * 4;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4; i < count; i += stride) {
+    if (i + 4 <= count) {
+      typename SrcTag::elem v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = src[i + k];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst[i + k] = DstTag::from_f32(SrcTag::to_f32(v[k]));
+    } else {
+      for (int64_t k = i; k < count; ++k) dst[k] = DstTag::from_f32(SrcTag::to_f32(src[k]));
+    }
+  }
+}
+
+template <typename SrcTag>
+int launch_convert(const void *src, void *dst, int32_t dst_dtype, int64_t count, hipStream_t s) {
+  const int grid = static_cast<int>(std::min<int64_t>(std::max<int64_t>(ceil_div(count, kThreads * 4), 1), 1 << 16));
+  const auto *in = static_cast<const typename SrcTag::elem *>(src);
+  switch (dst_dtype) {
+    case FLARE_FLOAT32: convert_kernel<SrcTag, TagF32><<<grid, kThreads, 0, s>>>(in, static_cast<float *>(dst), count); break;
+    case FLARE_FLOAT16: convert_kernel<SrcTag, TagF16><<<grid, kThreads, 0, s>>>(in, static_cast<_Float16 *>(dst), count); break;
+    case FLARE_BFLOAT16: convert_kernel<SrcTag, TagBF16><<<grid, kThreads, 0, s>>>(in, static_cast<uint16_t *>(dst), count); break;
+    default: return fail(FLARE_ERR_DTYPE, "conversion target must be float32, float16 or bfloat16, got dtype code %d", dst_dtype);
+  }
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
 }  // namespace
 }  // namespace flare
 
 using namespace flare;
+
+extern "C" int flare_convert(const void *src, int32_t src_dtype, void *dst, int32_t dst_dtype, int64_t count,
+                             void *stream) {
+  if (count < 0) return fail(FLARE_ERR_SHAPE, "element count %lld is negative", static_cast<long long>(count));
+  if (storage_bytes(src_dtype) == 0 || storage_bytes(dst_dtype) == 0)
+    return fail(FLARE_ERR_DTYPE, "conversion supports float32, float16 and bfloat16, got dtype codes %d -> %d",
+                src_dtype, dst_dtype);
+  if (count == 0) return FLARE_OK;
+  if (!src || !dst) return fail(FLARE_ERR_ARGUMENT, "conversion buffers are null");
+  hipStream_t s = as_stream(stream);
+  switch (src_dtype) {
+    case FLARE_FLOAT32: return launch_convert<TagF32>(src, dst, dst_dtype, count, s);
+    case FLARE_FLOAT16: return launch_convert<TagF16>(src, dst, dst_dtype, count, s);
+    default: return launch_convert<TagBF16>(src, dst, dst_dtype, count, s);
+  }
+}
 
 extern "C" int flare_zero_bytes(void *dst, int64_t bytes, void *stream) {
   if (bytes < 0) return fail(FLARE_ERR_SHAPE, "byte count %lld is negative", static_cast<long long>(bytes));

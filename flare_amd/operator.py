@@ -8,7 +8,9 @@ return correctly shaped outputs without a launch (``:236-280``), and the pool
 reclaimer runs when ``execution_context`` exits (``gpu_cupy.py:526-537``).
 
 The kernels are hand-written HIP for gfx950 (``flare_amd/csrc``), reached
-through the C ABI in ``include/flare_amd.h``.  Extensions over the reference:
+through the C ABI in ``include/flare_amd.h``.  Results are ``DeviceArray``s,
+the CuPy array protocol the reference's callers use (numpy dtypes, ``astype``,
+``__cuda_array_interface__``, DLPack).  Extensions over the reference:
 bfloat16 storage, and ``pooling="mean" | "weighted"`` for ``gather_pooled``.
 """
 
@@ -21,6 +23,7 @@ from typing import Any, Protocol
 import torch
 
 from flare_amd import _native
+from flare_amd.array import DeviceArray
 from flare_amd.contracts import SparseEmbeddingOperator, SparsePooledWidths, pooled_sparse_widths
 from flare_amd.conversion import contiguous, storage_code, to_device
 
@@ -60,6 +63,11 @@ class _OperatorStream:
         self.torch_stream.synchronize()
 
     def __enter__(self):
+        # inputs the caller is still producing on its own stream are complete
+        # before this stream reads them
+        caller = torch.cuda.current_stream(self.torch_stream.device)
+        if caller != self.torch_stream:
+            self.torch_stream.wait_stream(caller)
         ctx = torch.cuda.stream(self.torch_stream)
         ctx.__enter__()
         self._ctx.append(ctx)
@@ -110,20 +118,20 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
             tensor = tensor.to(torch.int32)
         return tensor
 
-    def array(self, value: Any) -> torch.Tensor:
+    def array(self, value: Any) -> DeviceArray:
         with self.stream:
-            return self._array_on_stream(value)
+            return DeviceArray(self._array_on_stream(value))
 
-    def inverse(self, value: Any) -> torch.Tensor:
+    def inverse(self, value: Any) -> DeviceArray:
         with self.stream:
-            return self._inverse_on_stream(value)
+            return DeviceArray(self._inverse_on_stream(value))
 
     def _workspace(self, nbytes: int) -> torch.Tensor:
         return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=self.device)
 
     # ------------------------------------------------------------------ forward
     def gather(self, emb_flat: Any, inverse: Any, batch_size: int, emb_dim: int,
-               pad_index: int) -> torch.Tensor:
+               pad_index: int) -> DeviceArray:
         with self.stream:
             embedding = contiguous(self._array_on_stream(emb_flat).reshape(-1, emb_dim))
             inverse = contiguous(self._inverse_on_stream(inverse).reshape(-1))
@@ -136,16 +144,16 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
                 )
             output = torch.empty((slots, emb_dim), dtype=embedding.dtype, device=self.device)
             if slots * emb_dim == 0:
-                return output.reshape(batch_size, 0, emb_dim)
+                return DeviceArray(output.reshape(batch_size, 0, emb_dim))
             _native.call(
                 "flare_gather", embedding.data_ptr(), code, embedding.shape[0], emb_dim,
                 inverse.data_ptr(), slots, int(pad_index), output.data_ptr(), self.stream.ptr,
             )
-            return output.reshape(batch_size, -1, emb_dim)
+            return DeviceArray(output.reshape(batch_size, -1, emb_dim))
 
     def gather_pooled(self, emb_flat: Any, inverse: Any, batch_size: int, emb_dim: int,
                       target_widths: SparsePooledWidths, pad_index: int, *,
-                      pooling: str = "sum", per_sample_weights: Any = None) -> torch.Tensor:
+                      pooling: str = "sum", per_sample_weights: Any = None) -> DeviceArray:
         with self.stream:
             feature_count, max_elements = pooled_sparse_widths(target_widths)
             embedding = contiguous(self._array_on_stream(emb_flat).reshape(-1, emb_dim))
@@ -161,7 +169,7 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
             output = torch.empty((batch_size, feature_count, emb_dim), dtype=embedding.dtype,
                                  device=self.device)
             if batch_size * feature_count * emb_dim == 0:
-                return output
+                return DeviceArray(output)
             if inverse.numel() != batch_size * feature_count * max_elements:
                 raise ValueError(
                     "pooled gather inverse slots must match batch_size * features * max_elements"
@@ -179,11 +187,11 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
                 _POOLING[pooling], None if weights is None else weights.data_ptr(),
                 output.data_ptr(), self.stream.ptr,
             )
-            return output
+            return DeviceArray(output)
 
     # ------------------------------------------------------------------ backward
     def scatter(self, emb_rows: int, emb_dim: int, inverse: Any, pad_index: int,
-                gradient: Any) -> torch.Tensor:
+                gradient: Any) -> DeviceArray:
         with self.stream:
             inverse = contiguous(self._inverse_on_stream(inverse).reshape(-1))
             gradient = contiguous(
@@ -200,10 +208,10 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
                 gradient.data_ptr(), output.data_ptr(), workspace.data_ptr(), nbytes,
                 self.stream.ptr,
             )
-            return output
+            return DeviceArray(output)
 
     def scatter_pooled(self, emb_rows: int, emb_dim: int, inverse: Any, pad_index: int,
-                       gradient: Any, target_widths: SparsePooledWidths) -> torch.Tensor:
+                       gradient: Any, target_widths: SparsePooledWidths) -> DeviceArray:
         with self.stream:
             feature_count, max_elements = pooled_sparse_widths(target_widths)
             inverse = contiguous(self._inverse_on_stream(inverse).reshape(-1))
@@ -224,7 +232,7 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
                 int(pad_index), gradient.data_ptr(), pooled_slots // feature_count, feature_count,
                 max_elements, output.data_ptr(), workspace.data_ptr(), nbytes, self.stream.ptr,
             )
-            return output
+            return DeviceArray(output)
 
     # ------------------------------------------------------------------ lifecycle
     def execution_context(self) -> AbstractContextManager[Any]:

@@ -54,6 +54,48 @@ def _raise_if_nonfinite(flag: torch.Tensor, stream: torch.cuda.Stream) -> None:
         raise FloatingPointError(_NONFINITE_MESSAGE)
 
 
+class _Ordered:
+    """Runs a call's work on ``stream`` ordered against the caller's current stream.
+
+    Entering makes ``stream`` wait for the caller's stream (inputs the caller
+    is still producing there are complete before the store reads them) and
+    makes ``stream`` current; leaving makes the caller's stream wait for
+    ``stream`` (the results are ready for whatever the caller enqueues next).
+    ``hold`` marks caller tensors the store reads or keeps as used by ``stream``
+    and ``give`` marks results as used by the caller's stream, so the caching
+    allocator reuses neither block while the other stream may still touch it.
+    """
+
+    def __init__(self, stream: torch.cuda.Stream, device: torch.device):
+        self.stream = stream
+        self.device = device
+        self.caller: torch.cuda.Stream | None = None
+        self._ctx = None
+
+    def __enter__(self) -> "_Ordered":
+        self.caller = torch.cuda.current_stream(self.device)
+        if self.caller != self.stream:
+            self.stream.wait_stream(self.caller)
+        self._ctx = torch.cuda.stream(self.stream)
+        self._ctx.__enter__()
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self._ctx.__exit__(*exc)
+        if self.caller != self.stream:
+            self.caller.wait_stream(self.stream)
+
+    def hold(self, *tensors: Any) -> None:
+        for t in tensors:
+            if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+                t.record_stream(self.stream)
+
+    def give(self, *tensors: Any) -> None:
+        for t in tensors:
+            if isinstance(t, torch.Tensor) and t.device.type == "cuda" and self.caller != self.stream:
+                t.record_stream(self.caller)
+
+
 # ----------------------------------------------------------------------------
 # optimizer and initializer configs (se.Adam / se.Sgd / se.Uniform / se.Zeros)
 # ----------------------------------------------------------------------------
@@ -246,6 +288,7 @@ class EmbeddingStore:
             }
         self._pending: dict[int, list[tuple[torch.Tensor, torch.Tensor]]] = {}
         self._workspace = _Workspace(self.device)
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)  # tables initialized
 
     # -- metadata -------------------------------------------------------------
     def value_dtype(self) -> str:
@@ -284,8 +327,9 @@ class EmbeddingStore:
     def lookup(self, keys: Any, dim: int):
         """Rows of ``keys`` as a ``[n, dim]`` tensor of the value dtype (DLPack producer)."""
         table = self._table(dim)
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             k = self._keys(keys)
+            order.hold(k)
             out = torch.empty((k.numel(), table.dim), dtype=table.table.dtype, device=self.device)
             if k.numel():
                 inv = contiguous(torch.clamp(k, -1, table.rows).to(torch.int32))
@@ -294,6 +338,7 @@ class EmbeddingStore:
                     table.rows, table.dim, inv.data_ptr(), k.numel(), table.rows + 1,
                     out.data_ptr(), int(self.stream.cuda_stream),
                 )
+            order.give(out)
         return out, None
 
     def lookup_or_insert(self, keys: Any, dim: int):
@@ -305,9 +350,10 @@ class EmbeddingStore:
         """Keyed gradients in float32 or bfloat16 transport (others are cast to float32).  With
         ``validate_values`` a non-finite gradient raises ``FloatingPointError`` here, before
         anything accumulates (synchronizes)."""
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             k = self._keys(keys)
             g = _transport_grad(to_device(grad, self.device))
+            order.hold(k, g)  # kept in _pending until optimizer_step
             if g.dim() != 2 or g.shape[0] != k.numel():
                 raise ValueError(
                     f"gradient shape {tuple(g.shape)} does not match {k.numel()} keys"
@@ -323,7 +369,7 @@ class EmbeddingStore:
     def optimizer_step(self, normalization_steps: int) -> None:
         if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
             raise ValueError("normalization_steps must be a positive integer")
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device):
             for dim, items in self._pending.items():
                 table = self._table(dim)
                 keys = items[0][0] if len(items) == 1 else torch.cat([k for k, _ in items])
@@ -421,7 +467,7 @@ class EmbeddingStore:
 
     def export_page_images(self, page_keys: int = 1 << 20) -> list[dict]:
         pages = []
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device):
             for dim, table in self.tables.items():
                 keys, rows = self._stored(dim)
                 for lo in range(0, int(keys.numel()), int(page_keys)):
@@ -431,7 +477,7 @@ class EmbeddingStore:
 
     def import_page_images(self, pages) -> None:
         """Writes every page's rows (values, optimizer state, steps) for its keys."""
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device):
             for page in pages:
                 dim = int(page["embedding_dim"])
                 table = self._table(dim)
@@ -455,12 +501,14 @@ class EmbeddingStore:
 
     def assign(self, keys: Any, values: Any) -> None:
         """Sets the rows of ``keys`` (inserting them in a dynamic store) to ``values [n, dim]``."""
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             v = to_device(values, self.device)
+            order.hold(v)
             if v.dim() != 2:
                 raise ValueError(f"assign needs values of shape [keys, dim], got {tuple(v.shape)}")
             table = self._table(int(v.shape[1]))
             k = self._keys(keys)
+            order.hold(k)
             if v.shape[0] != k.numel():
                 raise ValueError(f"values shape {tuple(v.shape)} does not match {k.numel()} keys")
             rows = self._rows_of(k, table.dim, insert=True)
@@ -543,6 +591,7 @@ class DynamicEmbeddingStore(EmbeddingStore):
         with torch.cuda.stream(self.stream):
             self.maps = {d: _KeyMap(_map_slots(self.capacity), self.device, self.stream) for d in self.tables}
         self._map_workspace = _Workspace(self.device)
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
 
     # -- keys -> rows -----------------------------------------------------------
     def _resolve(self, keys: torch.Tensor, dim: int, insert: bool, values: bool):
@@ -565,17 +614,27 @@ class DynamicEmbeddingStore(EmbeddingStore):
 
     def rows(self, keys: Any, dim: int, *, insert: bool = False) -> torch.Tensor:
         """Row of every key in ``dim``'s table (int32, -1 when absent)."""
-        with torch.cuda.stream(self.stream):
-            return self._resolve(self._keys(keys), dim, insert, values=False)[0]
+        with _Ordered(self.stream, self.device) as order:
+            k = self._keys(keys)
+            order.hold(k)
+            rows = self._resolve(k, dim, insert, values=False)[0]
+            order.give(rows)
+            return rows
+
+    def _values(self, keys: Any, dim: int, insert: bool):
+        with _Ordered(self.stream, self.device) as order:
+            k = self._keys(keys)
+            order.hold(k)
+            out = self._resolve(k, dim, insert, values=True)[1]
+            order.give(out)
+            return out, None
 
     def lookup(self, keys: Any, dim: int):
         """Rows of present keys, zeros for absent ones (``[n, dim]``, value dtype)."""
-        with torch.cuda.stream(self.stream):
-            return self._resolve(self._keys(keys), dim, False, values=True)[1], None
+        return self._values(keys, dim, False)
 
     def lookup_or_insert(self, keys: Any, dim: int):
-        with torch.cuda.stream(self.stream):
-            return self._resolve(self._keys(keys), dim, True, values=True)[1], None
+        return self._values(keys, dim, True)
 
     def contains(self, keys: Any, dim: int | None = None) -> np.ndarray:
         d = next(iter(self.tables)) if dim is None else int(dim)
@@ -598,7 +657,7 @@ class DynamicEmbeddingStore(EmbeddingStore):
         capacity = int(capacity)
         if capacity <= table.rows:
             return
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device):
             table.grow(capacity)
             old = self.maps[int(dim)]
             slots = _map_slots(capacity)
@@ -631,11 +690,12 @@ class DynamicEmbeddingStore(EmbeddingStore):
     def accumulate_gradients(self, keys: Any, grad: Any) -> None:
         """Keys must have rows (looked up or inserted before); others set device error bit 1
         and their gradient is dropped at ``optimizer_step``."""
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             g = to_device(grad, self.device)
             if g.dim() != 2:
                 raise ValueError(f"gradient must be [keys, dim], got shape {tuple(g.shape)}")
             k = self._keys(keys)
+            order.hold(g, k)
             if g.shape[0] != k.numel():
                 raise ValueError(f"gradient shape {tuple(g.shape)} does not match {k.numel()} keys")
             rows = self._resolve(k, int(g.shape[1]), False, values=False)[0].to(torch.int64)
@@ -683,6 +743,7 @@ class PooledTableShard:
                                      optimizer if optimizer is not None else RowWiseAdagrad(),
                                      initializer, generator, self.device)
         self._workspace = _Workspace(self.device)
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)  # table initialized
 
     @property
     def table(self) -> torch.Tensor:
@@ -721,9 +782,10 @@ class PooledTableShard:
     def lookup_pooled(self, ids: Any, offsets: Any, batch_size: int, *, pooling: str = "sum",
                       per_sample_weights: Any = None, out: torch.Tensor | None = None) -> torch.Tensor:
         """Forward: pooled rows in the storage dtype, ``pooled_shape(batch_size)``."""
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             ids_t, off = self._csr(ids, offsets, batch_size)
             w = self._weights(pooling, per_sample_weights, ids_t.numel())
+            order.hold(ids_t, off, w, out)
             if out is None:
                 out = torch.empty(self.pooled_shape(batch_size), dtype=self.state.table.dtype,
                                   device=self.device)
@@ -735,17 +797,19 @@ class PooledTableShard:
                 self.row_base.data_ptr(), _POOLING[pooling], self._layout_code,
                 None if w is None else w.data_ptr(), out.data_ptr(), int(self.stream.cuda_stream),
             )
+            order.give(out)
         return out
 
     def _backward(self, ids, offsets, batch_size, pooled_grad, pooling, per_sample_weights,
                   normalization_steps, optimizer_override, want_dedup, validate_values=False):
         if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or normalization_steps <= 0:
             raise ValueError("normalization_steps must be a positive integer")
-        with torch.cuda.stream(self.stream):
+        with _Ordered(self.stream, self.device) as order:
             ids_t, off = self._csr(ids, offsets, batch_size)
             n = int(ids_t.numel())
             w = self._weights(pooling, per_sample_weights, n)
             g = _transport_grad(to_device(pooled_grad, self.device))
+            order.hold(ids_t, off, w, g)
             if g.numel() != batch_size * self.num_tables * self.dim:
                 raise ValueError(f"pooled gradient must be {list(self.pooled_shape(batch_size))} "
                                  f"({self.layout} layout)")
@@ -778,6 +842,7 @@ class PooledTableShard:
             else:
                 self._dedup_apply(ids_t, id_code, n, off, batch_size, pooling, w, g, opt, flag,
                                   normalization_steps, grad_out, unique, inverse, first, count, ws, nbytes)
+            order.give(grad_out, unique, inverse, first, count)
         if flag is not None:
             _raise_if_nonfinite(flag, self.stream)
         if unique is None:
@@ -846,7 +911,10 @@ class PooledStepPlan:
     writes ``unique`` / ``first_indices`` / ``unique_count`` (device);
     ``apply(pooled_grad)`` reduces the gradient, updates the rows and writes
     ``inverse``.  No call allocates or synchronizes, so a loop of steps stays
-    asynchronous on the shard's stream.
+    asynchronous on the shard's stream.  Called with another stream current,
+    each call first makes the shard's stream wait for it and then makes it wait
+    for the shard's stream; under ``torch.cuda.stream(shard.stream)`` there is
+    nothing to order.
     """
 
     def __init__(self, shard: PooledTableShard, ids: Any, offsets: Any, batch_size: int,
@@ -872,6 +940,7 @@ class PooledStepPlan:
         self._id_code = _native.INT32 if self.ids.dtype == torch.int32 else _native.INT64
         self._stream = int(shard.stream.cuda_stream)
         self._dedup_stream: torch.cuda.Stream | None = None
+        torch.cuda.current_stream(dev).wait_stream(shard.stream)
 
     def step(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
              grad_out: torch.Tensor | None = None, optimizer: Any = None) -> torch.Tensor:
@@ -896,8 +965,20 @@ class PooledStepPlan:
         self.apply(pooled_grad, normalization_steps, grad_out, optimizer)
         return pooled
 
+    def _enter(self) -> torch.cuda.Stream:
+        """The caller's current stream, which the shard's stream now waits for."""
+        caller = torch.cuda.current_stream(self.shard.device)
+        if caller != self.shard.stream:
+            self.shard.stream.wait_stream(caller)
+        return caller
+
+    def _leave(self, caller: torch.cuda.Stream) -> None:
+        if caller != self.shard.stream:
+            caller.wait_stream(self.shard.stream)
+
     def forward(self) -> torch.Tensor:
         s = self.shard
+        caller = self._enter()
         _native.call(
             "flare_gather_pooled_csr", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
             s.total_rows, s.dim, self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
@@ -905,10 +986,13 @@ class PooledStepPlan:
             None if self.weights is None else self.weights.data_ptr(), self.pooled.data_ptr(),
             self._stream,
         )
+        self._leave(caller)
         return self.pooled
 
     def dedup(self) -> None:
+        caller = self._enter()
         self._dedup_on(self._stream)
+        self._leave(caller)
 
     def _dedup_on(self, stream: int) -> None:
         s = self.shard
@@ -932,6 +1016,11 @@ class PooledStepPlan:
                              f"device tensor ({s.layout} layout)")
         opt = s.state.native_optimizer if optimizer is None else optimizer
         s0, s1, st = s.state.pointers()
+        caller = self._enter()
+        if caller != s.stream:
+            pooled_grad.record_stream(s.stream)
+            if grad_out is not None:
+                grad_out.record_stream(s.stream)
         _native.call(
             "flare_pooled_apply_ex", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
             s.total_rows, s.dim, s0, s1, st, ctypes.byref(opt), self.n, s.num_tables, self.batch,
@@ -941,5 +1030,6 @@ class PooledStepPlan:
             None if grad_out is None else grad_out.data_ptr(), self.inverse.data_ptr(),
             self.workspace.data_ptr(), self.workspace_bytes, self._stream,
         )
+        self._leave(caller)
         if validate_values:
             _raise_if_nonfinite(self.nonfinite, s.stream)

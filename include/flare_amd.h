@@ -373,6 +373,15 @@ int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int64_t dst_ro
  * zeroes the outputs of its atomic scatters (:422-524). */
 int flare_zero_bytes(void *dst, int64_t bytes, void *stream);
 
+/* dst[i] = src[i] converted between float32, float16 and bfloat16 (widening
+ * exact, narrowing round-to-nearest-even) for count elements.  The transport
+ * casts of the reference's callers run on it: the keyed gradient sum cast to
+ * the bf16 wire dtype (recipes/recsys/ranking/workers/train_worker.py:518-522)
+ * and the bf16 -> fp32 native cast (src/flare/runtime/sparse_precision.py:
+ * 150-192), as the CuPy backend's astype does (gpu_cupy.py:434,474). */
+int flare_convert(const void *src, int32_t src_dtype, void *dst, int32_t dst_dtype,
+                  int64_t count, void *stream);
+
 /* A non-blocking stream at default priority, as the CuPy backend keeps one
  * per operator (src/flare/kernels/backends/gpu_cupy.py:253), for hosts with
  * no HIP runtime binding of their own; synchronize and destroy it with the

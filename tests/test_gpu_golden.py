@@ -26,7 +26,12 @@ def load(name: str):
     return np.load(GOLDEN / name, allow_pickle=False)
 
 
-def _host(t: torch.Tensor) -> np.ndarray:
+def _host(t) -> np.ndarray:
+    """Host copy of a torch tensor or of the operator's DeviceArray (bf16 as raw bits)."""
+    from flare_amd.array import DeviceArray
+
+    if isinstance(t, DeviceArray):
+        t = t.tensor
     if t.dtype == torch.bfloat16:
         return t.view(torch.int16).cpu().numpy().view(np.uint16)
     return t.cpu().numpy()
@@ -60,14 +65,14 @@ def test_gather_pooled_reference_cases(gpu_device, no_device_errors):
     op = HipSparseEmbeddingOperator("float32", "float32", empty_cache=False)
     out = op.gather_pooled(torch.from_numpy(f["f32_emb"]).to(gpu_device), f["f32_inverse"], 4, 2, (1, 1), 4)
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy(), f["f32_expected"])
+    np.testing.assert_array_equal(_host(out), f["f32_expected"])
     op = HipSparseEmbeddingOperator("float16", "float32", empty_cache=False)
     for emb, inv, exp, batch, dim, widths, pad in (("f16_emb", "f16_inverse", "f16_expected", 2, 2, (1, 2), 2),
                                                    ("f16_wide_emb", "f16_wide_inverse", "f16_wide_expected",
                                                     1, 1, (1, 3), 3)):
         out = op.gather_pooled(torch.from_numpy(f[emb]).to(gpu_device), f[inv], batch, dim, widths, pad)
         op.stream.synchronize()
-        np.testing.assert_array_equal(out.cpu().numpy(), f[exp])
+        np.testing.assert_array_equal(_host(out), f[exp])
     no_device_errors()
 
 
@@ -105,7 +110,7 @@ def test_scatter_pooled_matches_add_at(gpu_device, no_device_errors):
         grad = torch.from_numpy(f[f"case{k}_grad"]).to(gpu_device)
         got = op.scatter_pooled(rows, dim, inverse, rows, grad, (features, max_el))
         op.stream.synchronize()
-        np.testing.assert_allclose(got.cpu().numpy(), f[f"case{k}_expected"], rtol=2e-4, atol=2e-4)
+        np.testing.assert_allclose(_host(got), f[f"case{k}_expected"], rtol=2e-4, atol=2e-4)
     no_device_errors()
 
 

@@ -23,7 +23,12 @@ def _op(value_dtype="float32"):
     return HipSparseEmbeddingOperator(value_dtype, "float32", empty_cache=False)
 
 
-def _host(t: torch.Tensor) -> np.ndarray:
+def _host(t) -> np.ndarray:
+    """Host copy of a torch tensor or of the operator's DeviceArray (bf16 as raw bits)."""
+    from flare_amd.array import DeviceArray
+
+    if isinstance(t, DeviceArray):
+        t = t.tensor
     if t.dtype == torch.bfloat16:
         return t.view(torch.int16).cpu().numpy().view(np.uint16)
     return t.cpu().numpy()
@@ -48,7 +53,7 @@ def test_pooled_gather_known_answer(gpu_device, no_device_errors):
     inv = torch.tensor([0, 4, 2, 1], dtype=torch.int32, device=gpu_device)
     out = op.gather_pooled(emb, inv, 4, 2, (1, 1), 4)
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy().reshape(4, 2),
+    np.testing.assert_array_equal(_host(out).reshape(4, 2),
                                   [[0.0, 1.0], [0.0, 0.0], [4.0, 5.0], [2.0, 3.0]])
     no_device_errors()
 
@@ -59,18 +64,18 @@ def test_fp16_pooled_gather_known_answers(gpu_device, no_device_errors):
     emb = torch.tensor([[1.5, 2.0], [3.0, 4.0]], dtype=torch.float16, device=gpu_device)
     out = op.gather_pooled(emb, np.asarray([0, 1, 2, 2], np.int32), 2, 2, (1, 2), 2)
     op.stream.synchronize()
-    assert out.dtype == torch.float16
-    np.testing.assert_array_equal(out.cpu().numpy(), np.asarray([[[4.5, 6.0]], [[0.0, 0.0]]], np.float16))
+    assert out.dtype == np.float16
+    np.testing.assert_array_equal(_host(out), np.asarray([[[4.5, 6.0]], [[0.0, 0.0]]], np.float16))
     # :175-183 wide accumulation: 40000 - 40000 + 1 -> 1
     emb = torch.tensor([[40000.0], [-40000.0], [1.0]], dtype=torch.float16, device=gpu_device)
     out = op.gather_pooled(emb, np.asarray([0, 1, 2], np.int32), 1, 1, (1, 3), 3)
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy(), np.asarray([[[1.0]]], np.float16))
+    np.testing.assert_array_equal(_host(out), np.asarray([[[1.0]]], np.float16))
     # :225-233 overflow to inf
     emb = torch.tensor([[65504.0], [65504.0]], dtype=torch.float16, device=gpu_device)
     out = op.gather_pooled(emb, np.asarray([0, 1], np.int32), 1, 1, (1, 2), 2)
     op.stream.synchronize()
-    assert torch.isinf(out).all()
+    assert np.isinf(_host(out)).all()
     no_device_errors()
 
 
@@ -80,7 +85,7 @@ def test_empty_inputs_return_shapes_without_launch(gpu_device):
     inv = torch.empty((0,), dtype=torch.int32, device=gpu_device)
     assert tuple(op.gather_pooled(emb, inv, 0, 2, (1, 2), 0).shape) == (0, 1, 2)
     g = op.gather(emb, inv, 0, 2, 0)
-    assert tuple(g.shape) == (0, 0, 2) and g.dtype == torch.float16
+    assert tuple(g.shape) == (0, 0, 2) and g.dtype == np.float16
 
 
 @pytest.mark.parametrize("storage", ["float32", "float16", "bfloat16"])
@@ -137,7 +142,7 @@ def test_scatter_pooled_matches_duplicate_key_sum(gpu_device, no_device_errors, 
     actual = op.scatter_pooled(rows, dim, torch.from_numpy(inverse).to(gpu_device), rows,
                                torch.from_numpy(gradient).to(gpu_device), (feature_count, max_elements))
     op.stream.synchronize()
-    got = actual.cpu().numpy()
+    got = _host(actual)
     np.testing.assert_allclose(got, expected, atol=2e-4, rtol=2e-4)
     # bit-exact against the oracle's (documented) reduction order
     exact = O.scatter_pooled(rows, dim, inverse, rows, gradient, (feature_count, max_elements))
@@ -168,8 +173,8 @@ def test_scatter_exact_counts(gpu_device, no_device_errors):
                                 (feature_count, max_elements))
         op.stream.synchronize()
         expected = np.broadcast_to((counts / (256 * (2 ** index)))[:, None], (rows, width))
-        np.testing.assert_array_equal(out.cpu().numpy(), expected)
-        np.testing.assert_array_equal(out.to(torch.bfloat16).to(torch.float32).cpu().numpy(), expected)
+        np.testing.assert_array_equal(_host(out), expected)
+        np.testing.assert_array_equal(_host(out.astype("bfloat16").astype("float32")), expected)
     no_device_errors()
 
 
@@ -181,7 +186,7 @@ def test_scatter_matches_oracle(gpu_device, no_device_errors, slots, rows, dim, 
     op = _op()
     out = op.scatter(rows, dim, torch.from_numpy(inv).to(gpu_device), rows, torch.from_numpy(grad).to(gpu_device))
     op.stream.synchronize()
-    got = out.cpu().numpy()
+    got = _host(out)
     np.testing.assert_array_equal(got, O.scatter(rows, dim, inv, rows, grad))
     # and within tolerance of plain slot-order (Numba reference order) sums
     ref = O.scatter(rows, dim, inv, rows, grad, unit=max(slots, 1))
@@ -194,7 +199,7 @@ def test_gather_out_of_range_ids_are_zero_and_flagged(gpu_device, no_device_erro
     emb = torch.ones((4, 2), dtype=torch.float32, device=gpu_device)
     out = op.gather(emb, torch.tensor([0, 9, -3, 4], dtype=torch.int32, device=gpu_device), 4, 2, 4)
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy().reshape(4, 2), [[1, 1], [0, 0], [0, 0], [0, 0]])
+    np.testing.assert_array_equal(_host(out).reshape(4, 2), [[1, 1], [0, 0], [0, 0], [0, 0]])
     no_device_errors(expected=1)
 
 
@@ -210,7 +215,7 @@ def test_scatter_hot_key_across_many_units_bit_exact(gpu_device, no_device_error
     out = op.scatter(rows, dim, torch.from_numpy(inverse).to(gpu_device), rows,
                      torch.from_numpy(grad).to(gpu_device))
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy(), O.scatter(rows, dim, inverse, rows, grad))
+    np.testing.assert_array_equal(_host(out), O.scatter(rows, dim, inverse, rows, grad))
     no_device_errors()
 
 
@@ -230,11 +235,11 @@ def test_scatter_key_past_the_fold_chunk_bit_exact(gpu_device, no_device_errors,
     out = op.scatter(rows, dim, torch.from_numpy(inverse).to(gpu_device), rows,
                      torch.from_numpy(grad).to(gpu_device))
     op.stream.synchronize()
-    np.testing.assert_array_equal(out.cpu().numpy(), O.scatter(rows, dim, inverse, rows, grad))
+    np.testing.assert_array_equal(_host(out), O.scatter(rows, dim, inverse, rows, grad))
     # exactly 64 units for one key: the one-level fold
     inv2 = np.full(64 * 64, 5, np.int32)
     g2 = rng.standard_normal((inv2.size, dim)).astype(np.float32)
     out2 = op.scatter(rows, dim, torch.from_numpy(inv2).to(gpu_device), rows, torch.from_numpy(g2).to(gpu_device))
     op.stream.synchronize()
-    np.testing.assert_array_equal(out2.cpu().numpy(), O.scatter(rows, dim, inv2, rows, g2))
+    np.testing.assert_array_equal(_host(out2), O.scatter(rows, dim, inv2, rows, g2))
     no_device_errors()
