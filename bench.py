@@ -201,6 +201,132 @@ def cpu_baseline(config: int, seconds: float) -> dict:
     }
 
 
+def full_size_check(shard, plan, w, grad, grad_out, none_opt, sample: int = 4096, seed: int = 7) -> dict:
+    """One more full-size step of ``plan``, checked (the oracle is the checker here, after timing).
+
+    - dedup invariants over all N occurrences: ``unique[inverse] == keys``,
+      ``keys[first] == unique``, ``first`` strictly increasing, ``U`` = distinct keys;
+    - ``sample`` random bags: pooled rows bit-exact against the oracle's pooling of the
+      rows they read (taken from the table before the step);
+    - ``sample`` random unique keys: their updated rows (within 1 ulp of the storage dtype)
+      and optimizer state (rtol 1e-5), or their reduced gradients (bit-exact), against the
+      oracle's segment sums in the same unit order and its optimizer;
+    - ``sample`` random rows no id touched: unchanged.
+    Rows are compared as gathered before and after the step, so no table is copied whole.
+    """
+    import numpy as np
+    import torch
+
+    from flare_amd import _native
+    from oracle import sparse_oracle as O
+
+    dev = shard.device
+    stream = shard.stream
+    rng = np.random.default_rng(seed)
+    keys = w.global_keys()
+    lengths = np.diff(w.offsets)
+    bag_of = np.repeat(np.arange(w.num_tables * w.batch, dtype=np.int64), lengths)
+    perm, sk, starts = O.sorted_occurrences(keys)
+    ends = np.append(starts[1:], perm.size)
+    seg_keys = sk[starts]
+    pick = np.sort(rng.choice(starts.size, size=min(sample, starts.size), replace=False))
+    check_rows = seg_keys[pick]
+    touched = np.zeros(w.total_rows, dtype=bool)
+    touched[seg_keys] = True
+    free = np.nonzero(~touched)[0]
+    still_rows = rng.choice(free, size=min(sample, free.size), replace=False) if free.size else free
+    nbags = w.num_tables * w.batch
+    bags = np.sort(rng.choice(nbags, size=min(sample, nbags), replace=False))
+    st = shard.state
+
+    def rows_of(t, rows):
+        if t is None:
+            return None
+        idx = torch.from_numpy(np.asarray(rows, np.int64)).to(dev)
+        return t.index_select(0, idx)
+
+    def host(t):
+        if t is None:
+            return None
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    pooled_row = bags if shard.layout == "table_major" else (bags % w.batch) * w.num_tables + bags // w.batch
+    with torch.cuda.stream(stream):
+        bag_rows = np.unique(keys[np.concatenate([np.arange(w.offsets[k], w.offsets[k + 1]) for k in bags])])
+        before = {name: host(rows_of(t, check_rows)) for name, t in
+                  (("table", st.table), ("s0", st.state0), ("s1", st.state1), ("step", st.step))}
+        pool_src = host(rows_of(st.table, bag_rows))
+        still_before = host(rows_of(st.table, still_rows))
+        plan.forward()
+        plan.dedup()
+        plan.apply(grad, grad_out=grad_out, optimizer=none_opt)
+        after = {name: host(rows_of(t, check_rows)) for name, t in
+                 (("table", st.table), ("s0", st.state0), ("s1", st.state1), ("step", st.step))}
+        still_after = host(rows_of(st.table, still_rows))
+        pooled = host(plan.pooled.reshape(-1, w.dim)[torch.from_numpy(pooled_row).to(dev)])
+    errors = int(_native.library().flare_take_device_errors(int(stream.cuda_stream)))
+    u = int(plan.unique_count.item())
+    unique = plan.unique[:u].cpu().numpy()
+    inverse = plan.inverse[:w.num_ids].cpu().numpy()
+    first = plan.first_indices[:u].cpu().numpy()
+    out = {"device_errors": errors, "occurrences": int(keys.size), "unique": u}
+    out["unique_count_ok"] = u == int(starts.size)
+    out["unique_inverse_ok"] = bool(np.array_equal(unique[inverse], keys))
+    out["first_indices_ok"] = bool(np.array_equal(keys[first], unique) and np.all(np.diff(first) > 0))
+    # pooled rows of the sampled bags: the oracle pools the same rows (compact table)
+    sub_off = np.zeros(bags.size + 1, np.int64)
+    sub_off[1:] = np.cumsum(lengths[bags])
+    sub_keys = np.concatenate([keys[w.offsets[k]:w.offsets[k + 1]] for k in bags])
+    sub_ids = np.searchsorted(bag_rows, sub_keys)
+    sub_w = None if w.weights is None else np.concatenate([w.weights[w.offsets[k]:w.offsets[k + 1]] for k in bags])
+    expected = O.gather_pooled_csr(pool_src, sub_ids, sub_off, np.asarray([0, bag_rows.size], np.int64), bags.size,
+                                   w.dim, storage=w.value_dtype, pooling=w.pooling, weights=sub_w)
+    out["sampled_bags"] = int(bags.size)
+    out["pooled_bit_exact"] = bool(np.array_equal(pooled, expected.reshape(bags.size, w.dim)))
+    # reduced gradients of the sampled keys, in the kernels' unit order
+    positions = np.unique(np.concatenate([np.arange(a, e) for a, e in zip(starts[pick], ends[pick])]))
+    occ = perm[positions]
+    grow = bag_of[occ] if shard.layout == "table_major" else \
+        (bag_of[occ] % w.batch) * w.num_tables + bag_of[occ] // w.batch
+    g_rows = grad.reshape(-1, w.dim).index_select(0, torch.from_numpy(grow).to(dev)).float().cpu().numpy()
+    if w.pooling == "weighted":
+        g_rows = (g_rows * w.weights[occ][:, None]).astype(np.float32)
+    elif w.pooling == "mean":
+        g_rows = (g_rows / np.maximum(lengths[bag_of[occ]], 1).astype(np.float32)[:, None]).astype(np.float32)
+    sums = O.segment_sums_selected(lambda pos: g_rows[np.searchsorted(positions, pos)], starts[pick], ends[pick],
+                                   w.dim)
+    out["sampled_keys"] = int(pick.size)
+    if none_opt is not None:  # reduced gradients in first-occurrence order
+        rank = np.searchsorted(np.sort(unique), check_rows)
+        order = np.argsort(unique, kind="stable")
+        got = grad_out[:u][torch.from_numpy(order[rank]).to(dev)].cpu().numpy()
+        out["reduced_grad_bit_exact"] = bool(np.array_equal(got, sums))
+        ok_rows = out["reduced_grad_bit_exact"]
+    else:
+        w0 = O.storage_to_f32(before["table"], w.value_dtype)
+        if w.optimizer == "adam":
+            w1, m1, v1, s1 = O.adam_update(w0, before["s0"], before["s1"], before["step"], sums, lr=0.01)
+            state_pairs = [(after["s0"], m1), (after["s1"], v1)]
+            steps_ok = bool(np.array_equal(after["step"], s1))
+        else:
+            w1, acc1 = O.rowwise_adagrad_update(w0, before["s0"], sums, lr=0.01, eps=1e-8)
+            state_pairs = [(after["s0"], acc1)]
+            steps_ok = True
+        ulps = O.storage_ulp_distance(after["table"], O.f32_to_storage(w1, w.value_dtype), w.value_dtype)
+        rel = max(float(np.max(np.abs(a - b) / np.maximum(np.abs(b), 1e-30))) for a, b in state_pairs)
+        out["rows_max_ulp"] = int(ulps.max())
+        out["state_max_rel_err"] = rel
+        ok_rows = out["rows_max_ulp"] <= 1 and rel <= 1e-5 and steps_ok
+    out["untouched_rows"] = int(still_rows.size)
+    out["untouched_rows_unchanged"] = bool(np.array_equal(still_before, still_after))
+    out["passed"] = bool(errors == 0 and out["unique_count_ok"] and out["unique_inverse_ok"] and
+                         out["first_indices_ok"] and out["pooled_bit_exact"] and ok_rows and
+                         out["untouched_rows_unchanged"])
+    return out
+
+
 def _int64_key_sets(batches: int) -> list:
     """Unique ids of workload 5 batches (1e8-id space, 131072 bags of U[1,64] Zipf(1.05) ids)
     in first-occurrence order, mixed by the SplitMix64 output function into arbitrary int64
@@ -539,6 +665,8 @@ def main() -> int:
     ap.add_argument("--batches", type=int, default=8, help="pre-generated id batches to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-check", action="store_true",
+                    help="skip the full-size correctness check of one more step after timing")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="before timing, run a plain device-to-device copy of this many MiB three times "
                          "(a kernel of known traffic, to scale FETCH_SIZE / WRITE_SIZE counters)")
@@ -684,6 +812,14 @@ def main() -> int:
     wall1 = time.perf_counter()
     stream_ctx.__exit__(None, None, None)
     _native.check(lib.flare_set_update_events(None, 0))
+    timed_errors = int(lib.flare_take_device_errors(int(stream.cuda_stream)))
+    check = {"timed_steps_device_errors": timed_errors}
+    if not args.no_check:
+        t_check = time.time()
+        check.update(full_size_check(shard, plans[0], batches[0], grad, grad_out, none_opt))
+        check["seconds"] = round(time.time() - t_check, 1)
+        log(f"full-size check: {check}")
+    check["passed"] = bool(timed_errors == 0 and check.get("passed", True))
 
     kernel_bytes = [update_kernel_bytes(b, s) for b in batches]
     step_ms, fwd_ms, dedup_ms, apply_ms = [], [], [], []
@@ -773,6 +909,7 @@ def main() -> int:
         "roofline": dominant,
         "roofline_kernels": kernels,
         "cpu_baseline": None,
+        "check": check,
     }
     if not args.no_cpu_baseline:
         del plans, grad
@@ -782,6 +919,9 @@ def main() -> int:
         except Exception as error:  # the GPU result stands without the baseline
             log(f"cpu baseline failed: {error!r}")
     print(json.dumps(result), flush=True)
+    if not check["passed"]:
+        log("the full-size correctness check failed: the measured step is not valid")
+        return 1
     return 0
 
 

@@ -390,40 +390,36 @@ def sorted_occurrences(keys: np.ndarray, valid: np.ndarray | None = None):
 FOLD_CHUNK = 64  # unit partials per first-level fold run of a very hot key
 
 
-def segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int, unit: int = REDUCE_UNIT):
-    """Sum rows of ``contrib`` (already in sorted order) per segment, HIP order.
-
-    ``starts`` are segment heads in sorted positions; ``total`` = #positions.
-    Returns ``[len(starts), D]`` float32.
-    """
-    contrib = np.asarray(contrib, dtype=np.float32)
-    nseg = starts.size
-    dim = contrib.shape[1] if contrib.ndim == 2 else 0
-    ends = np.append(starts[1:], total)
-    out = np.zeros((nseg, dim), dtype=np.float32)
-    # sequential sum inside each (segment, unit) piece
-    piece_start = []
-    piece_seg = []
-    for s in range(nseg):
-        a, e = int(starts[s]), int(ends[s])
+def _segment_pieces(starts: np.ndarray, ends: np.ndarray, unit: int):
+    """Cut each segment [start, end) of sorted positions at multiples of ``unit``:
+    (segment of each piece, first absolute position, length)."""
+    piece_seg, piece_a, piece_len = [], [], []
+    for s, (a, e) in enumerate(zip(starts.tolist(), ends.tolist())):
         cut = a
         while cut < e:
             nxt = min(e, (cut // unit + 1) * unit)
-            piece_start.append((cut, nxt))
             piece_seg.append(s)
+            piece_a.append(cut)
+            piece_len.append(nxt - cut)
             cut = nxt
-    if not piece_seg:
+    return np.asarray(piece_seg, np.int64), np.asarray(piece_a, np.int64), np.asarray(piece_len, np.int64)
+
+
+def _segment_sums_by_pieces(rows_at, starts: np.ndarray, ends: np.ndarray, dim: int, unit: int) -> np.ndarray:
+    """Sums of the segments [starts, ends) (absolute sorted positions), HIP order:
+    sequential fp32 sums inside each (segment, unit) piece, then the pieces of each
+    segment folded left to right (a segment of more than FOLD_CHUNK pieces: each run
+    of FOLD_CHUNK pieces left to right, then the run results left to right).
+    ``rows_at(positions)`` returns the contribution rows at absolute positions."""
+    nseg = starts.size
+    out = np.zeros((nseg, dim), dtype=np.float32)
+    piece_seg, pa, plen = _segment_pieces(starts, ends, unit)
+    if piece_seg.size == 0:
         return out
-    piece_seg = np.asarray(piece_seg)
-    pa = np.asarray([p[0] for p in piece_start])
-    plen = np.asarray([p[1] - p[0] for p in piece_start])
     partial = np.zeros((pa.size, dim), dtype=np.float32)
     for step in range(int(plen.max())):
         act = np.nonzero(plen > step)[0]
-        partial[act] = (partial[act] + contrib[pa[act] + step]).astype(np.float32)
-    # fold pieces of each segment left to right (first piece is the seed); a
-    # segment of more than FOLD_CHUNK pieces folds each run of FOLD_CHUNK pieces
-    # left to right, then the run results left to right
+        partial[act] = (partial[act] + np.asarray(rows_at(pa[act] + step), np.float32)).astype(np.float32)
     first_piece = np.ones(pa.size, dtype=bool)
     first_piece[1:] = piece_seg[1:] != piece_seg[:-1]
     out[piece_seg[first_piece]] = partial[first_piece]
@@ -433,17 +429,38 @@ def segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int, unit: int 
         seg = piece_seg[s0]
         if c <= FOLD_CHUNK:
             acc = partial[s0].copy()
-            for p in range(s0 + 1, s0 + c):
-                acc = (acc + partial[p]).astype(np.float32)
+            for q in range(s0 + 1, s0 + c):
+                acc = (acc + partial[q]).astype(np.float32)
         else:
             acc = None
             for c0 in range(0, c, FOLD_CHUNK):
                 run = partial[s0 + c0].copy()
-                for p in range(s0 + c0 + 1, s0 + min(c0 + FOLD_CHUNK, c)):
-                    run = (run + partial[p]).astype(np.float32)
+                for q in range(s0 + c0 + 1, s0 + min(c0 + FOLD_CHUNK, c)):
+                    run = (run + partial[q]).astype(np.float32)
                 acc = run if acc is None else (acc + run).astype(np.float32)
         out[seg] = acc
     return out
+
+
+def segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int, unit: int = REDUCE_UNIT):
+    """Sum rows of ``contrib`` (already in sorted order) per segment, HIP order.
+
+    ``starts`` are segment heads in sorted positions; ``total`` = #positions.
+    Returns ``[len(starts), D]`` float32.
+    """
+    contrib = np.asarray(contrib, dtype=np.float32)
+    dim = contrib.shape[1] if contrib.ndim == 2 else 0
+    starts = np.asarray(starts, np.int64)
+    ends = np.append(starts[1:], total).astype(np.int64)
+    return _segment_sums_by_pieces(lambda pos: contrib[pos], starts, ends, dim, unit)
+
+
+def segment_sums_selected(rows_at, starts: np.ndarray, ends: np.ndarray, dim: int, unit: int = REDUCE_UNIT):
+    """``segment_sums`` of some segments only, each given by its absolute sorted positions
+    ``[starts[i], ends[i])`` within the whole sorted occurrence stream (the unit cuts depend
+    on those absolute positions); ``rows_at(positions)`` returns their contribution rows.
+    For checking a sample of keys of a step too large to sum in full on the host."""
+    return _segment_sums_by_pieces(rows_at, np.asarray(starts, np.int64), np.asarray(ends, np.int64), dim, unit)
 
 
 def sequential_segment_sums(contrib: np.ndarray, starts: np.ndarray, total: int):

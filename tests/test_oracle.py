@@ -355,3 +355,19 @@ def test_segment_sums_fold_order_changes_only_past_fold_chunk():
                 run0 = (run0 + x).astype(np.float32)
             expected = (run0 + sums[O.FOLD_CHUNK]).astype(np.float32)
             np.testing.assert_array_equal(out[0], expected)
+
+
+def test_segment_sums_selected_matches_the_full_sums():
+    """The sampled form used by bench.py's full-size check gives the full form's rows for the
+    selected segments, including keys crossing units and folding in runs (absolute positions)."""
+    rng = np.random.default_rng(9)
+    keys = np.concatenate([rng.integers(0, 40, 3000), np.full(9000, 17), rng.integers(0, 500, 2000)])
+    rng.shuffle(keys)
+    contrib = rng.normal(0, 1, size=(keys.size, 5)).astype(np.float32)
+    perm, sk, starts = O.sorted_occurrences(keys)
+    full = O.segment_sums(contrib[perm], starts, perm.size)
+    ends = np.append(starts[1:], perm.size)
+    pick = np.sort(rng.choice(starts.size, size=60, replace=False))
+    pick = np.union1d(pick, [int(np.nonzero(sk[starts] == 17)[0][0])])  # the hot key (> 64 units)
+    sel = O.segment_sums_selected(lambda pos: contrib[perm[pos]], starts[pick], ends[pick], 5)
+    np.testing.assert_array_equal(sel, full[pick])
