@@ -57,6 +57,8 @@ SIGNATURES = {
     "flare_scatter_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "flare_scatter": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "flare_scatter_pooled": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
+    "flare_scatter_ex": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "flare_scatter_pooled_ex": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i32, _vp, _sz, _vp]),
     "flare_unique_workspace_bytes": (_sz, [_i64, _i32]),
     "flare_unique_first_occurrence": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "flare_sparse_update_workspace_bytes": (_sz, [_i64, _i64, _i32]),

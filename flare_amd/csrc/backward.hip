@@ -392,11 +392,14 @@ template <typename SrcT, typename K>
 __global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__restrict__ src,
                                                              int64_t n,
                                                              const uint64_t *__restrict__ minimum,
-                                                             int passes, int digit, K *__restrict__ keys,
-                                                             uint32_t *__restrict__ hist) {
+                                                             uint64_t key_bound, int passes, int digit,
+                                                             K *__restrict__ keys,
+                                                             uint32_t *__restrict__ hist, int *err) {
   // minimum != nullptr: keys are mapped to their order-preserving unsigned
   // image and offset by the measured minimum; otherwise the caller promised
-  // 0 <= key < bound and the raw value is the key.
+  // 0 <= key < key_bound and the raw value is the key: a key outside that
+  // range (the sort only covers the bits of key_bound - 1, so its run could
+  // split) sets the index error bit.
   __shared__ uint32_t s_hist[kMaxHistBins];
   for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
   __syncthreads();
@@ -408,6 +411,10 @@ __global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__rest
       if (minimum) ord ^= 0x8000000000000000ull;
     } else {
       ord = static_cast<uint64_t>(src[i]);
+    }
+    if (!minimum) {
+      const bool negative = std::is_signed<SrcT>::value && static_cast<int64_t>(src[i]) < 0;
+      if (negative || ord >= key_bound) record_error(err, kErrIndexOutOfRange);
     }
     const K k = static_cast<K>(ord - lo);
     keys[i] = k;
@@ -898,7 +905,8 @@ struct UpdateArgs {
   float *sums;  // [runs][dim] per-key gradient sums (optimizer modes)
   const uint32_t *run_key;
   uint32_t *hot_runs;  // keys spanning more than kInlineSpan + 1 units (meta[2] of them)
-  float *out;
+  void *out;           // kModeRows / kModeUnique results: float32, or bfloat16 when out_bf16
+  int out_bf16;
   void *table;
   float *s0;
   float *s1;
@@ -948,6 +956,15 @@ __device__ __forceinline__ void load_ahead(const UpdateArgs &a, uint32_t r, uint
   }
 }
 
+// A finished keyed sum written to the output: float32, or rounded to nearest
+// even bfloat16 (the gradient transport dtype, train_worker.py:518-522) in the
+// same store that would have written the float32 row.
+template <int VEC>
+__device__ __forceinline__ void store_out(const UpdateArgs &a, int64_t at, const float (&x)[VEC]) {
+  if (a.out_bf16) store_from_f32<TagBF16, VEC>(static_cast<uint16_t *>(a.out) + at, x);
+  else store_f32<VEC>(static_cast<float *>(a.out) + at, x);
+}
+
 template <typename Tag, int VEC, int G, int NC, int MODE>
 __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, float (&g)[NC][VEC],
                                              const RowAhead<NC, VEC> &ahead, int lane) {
@@ -963,7 +980,7 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, 
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int col = (c * G + lane) * VEC;
-      if (col < D) store_f32<VEC>(a.out + row * D + col, g[c]);
+      if (col < D) store_out<VEC>(a, row * D + col, g[c]);
     }
   } else {
     using E = typename Tag::elem;
@@ -1220,12 +1237,13 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
     const bool whole = starts && ends_here;
     const uint64_t le = (pf == 63) ? ~0ull : ((2ull << pf) - 1);
     const int k = __popcll(heads & ~1ull & le);  // key index within the unit
-    float *dst;
+    float *dst = nullptr;
+    int64_t out_at = -1;  // kDirect whole keys: element offset of the key's output row
     if (whole) {
       if constexpr (MODE == kModeRows) {
-        dst = a.out + static_cast<int64_t>(s_dest[group][pf]) * D;
+        out_at = static_cast<int64_t>(s_dest[group][pf]) * D;
       } else if constexpr (MODE == kModeUnique) {
-        dst = a.out + static_cast<int64_t>(s_dest[group][k]) * D;
+        out_at = static_cast<int64_t>(s_dest[group][k]) * D;
       } else {
         dst = a.sums + static_cast<int64_t>(r0 + k) * D;
       }
@@ -1246,7 +1264,10 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[c][v] = acc[c][v] / a.norm;
       }
-      if (col < D) store_f32<VEC>(dst + col, acc[c]);
+      if (col < D) {
+        if (out_at >= 0) store_out<VEC>(a, out_at + col, acc[c]);
+        else store_f32<VEC>(dst + col, acc[c]);
+      }
 #pragma unroll
       for (int v = 0; v < VEC; ++v) acc[c][v] = 0.0f;
     }
@@ -1899,9 +1920,9 @@ bool vec4_ok(const void *p) { return aligned(p, 16); }
 // Shared tail of the keyed-row entry points (scatter, scatter_pooled, sparse_update).
 int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int *err, hipStream_t s, int mode,
                 int dtype, int dim, const void *grad, int grad_mode, uint32_t grad_div,
-                float *out, void *table, float *s0, float *s1, int32_t *step,
+                void *out, void *table, float *s0, float *s1, int32_t *step,
                 const flare_optimizer *opt, int32_t norm_steps, int grad_dtype = FLARE_FLOAT32,
-                int check_finite = 0, int32_t *nonfinite_out = nullptr) {
+                int check_finite = 0, int32_t *nonfinite_out = nullptr, int out_bf16 = 0) {
   int sorted = 0;
   FLARE_TRY(dedup_rows(w, plan, sentinel, err, s, &sorted, nullptr, nullptr, kUniqueNone, nullptr,
                        0, nullptr, nullptr));
@@ -1930,6 +1951,7 @@ int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, in
   a.run_key = w.run_key;
   a.hot_runs = w.hot_runs;
   a.out = out;
+  a.out_bf16 = out_bf16;
   a.table = table;
   a.s0 = s0;
   a.s1 = s1;
@@ -1967,18 +1989,17 @@ extern "C" size_t flare_scatter_workspace_bytes(int64_t slots, int64_t emb_rows,
 }
 
 static int scatter_common(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
-                          int32_t pad_index, const float *grad, uint32_t grad_div, float *out,
-                          void *workspace, size_t workspace_bytes, void *stream) {
+                          int32_t pad_index, const float *grad, uint32_t grad_div, void *out,
+                          int32_t out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
   if (dim <= 0 || emb_rows < 0 || slots < 0) return fail(FLARE_ERR_SHAPE, "invalid scatter sizes");
+  if (out_dtype != FLARE_FLOAT32 && out_dtype != FLARE_BFLOAT16)
+    return fail(FLARE_ERR_DTYPE, "scatter output dtype must be float32 or bfloat16, got dtype code %d", out_dtype);
   if (slots > kMaxOccurrences) return fail(FLARE_ERR_LIMIT, "too many inverse slots (%lld)", static_cast<long long>(slots));
   if (emb_rows >= 0xffffffffll) return fail(FLARE_ERR_LIMIT, "too many embedding rows");
   hipStream_t s = as_stream(stream);
-  if (emb_rows > 0) {
-    const size_t n = static_cast<size_t>(emb_rows) * dim;
-    const int grid = static_cast<int>(std::min<size_t>((n + 255) / 256, 8192));
-    zero_f32_kernel<<<std::max(grid, 1), 256, 0, s>>>(out, n);
-    FLARE_TRY_HIP(hipGetLastError());
-  }
+  const int out_bf16 = out_dtype == FLARE_BFLOAT16 ? 1 : 0;
+  if (emb_rows > 0)  // rows no slot reaches are zero (a zero fill kernel: capturable)
+    FLARE_TRY(flare_zero_bytes(out, emb_rows * static_cast<int64_t>(dim) * (out_bf16 ? 2 : 4), stream));
   if (slots == 0 || emb_rows == 0) return FLARE_OK;
   Workspace w = layout_workspace(workspace, slots, 4, dim, false, false, true);
   FLARE_TRY(check_workspace(w, workspace_bytes));
@@ -1996,14 +2017,34 @@ static int scatter_common(int64_t emb_rows, int32_t dim, const int32_t *inverse,
   FLARE_TRY_HIP(hipGetLastError());
   return reduce_rows(w, plan, sentinel, err, s, kModeRows, FLARE_FLOAT32, dim, grad,
                      grad_div == 1 ? kGradRowOcc : kGradRowDiv, grad_div, out, nullptr, nullptr,
-                     nullptr, nullptr, nullptr, 1);
+                     nullptr, nullptr, nullptr, 1, FLARE_FLOAT32, 0, nullptr, out_bf16);
 }
 
 extern "C" int flare_scatter(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
                              int32_t pad_index, const float *grad, float *out, void *workspace,
                              size_t workspace_bytes, void *stream) {
-  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad, 1, out, workspace,
+  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad, 1, out, FLARE_FLOAT32, workspace,
                         workspace_bytes, stream);
+}
+
+extern "C" int flare_scatter_ex(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
+                                int32_t pad_index, const float *grad, void *out, int32_t out_dtype,
+                                void *workspace, size_t workspace_bytes, void *stream) {
+  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad, 1, out, out_dtype, workspace,
+                        workspace_bytes, stream);
+}
+
+static int scatter_pooled_common(int64_t emb_rows, int32_t dim, const int32_t *inverse, int64_t slots,
+                                 int32_t pad_index, const float *grad, int64_t batch, int32_t features,
+                                 int32_t max_elements, void *out, int32_t out_dtype, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  if (features <= 0 || max_elements <= 0)
+    return fail(FLARE_ERR_WIDTH, "Sparse embedding pooled operations require positive target widths, got (%d, %d).", features, max_elements);
+  if (slots != batch * features * static_cast<int64_t>(max_elements))
+    return fail(FLARE_ERR_SHAPE, "pooled scatter inverse slots must match gradient rows times max_elements");
+  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad,
+                        static_cast<uint32_t>(max_elements), out, out_dtype, workspace, workspace_bytes,
+                        stream);
 }
 
 extern "C" int flare_scatter_pooled(int64_t emb_rows, int32_t dim, const int32_t *inverse,
@@ -2011,13 +2052,17 @@ extern "C" int flare_scatter_pooled(int64_t emb_rows, int32_t dim, const int32_t
                                     int64_t batch, int32_t features, int32_t max_elements,
                                     float *out, void *workspace, size_t workspace_bytes,
                                     void *stream) {
-  if (features <= 0 || max_elements <= 0)
-    return fail(FLARE_ERR_WIDTH, "Sparse embedding pooled operations require positive target widths, got (%d, %d).", features, max_elements);
-  if (slots != batch * features * static_cast<int64_t>(max_elements))
-    return fail(FLARE_ERR_SHAPE, "pooled scatter inverse slots must match gradient rows times max_elements");
-  return scatter_common(emb_rows, dim, inverse, slots, pad_index, grad,
-                        static_cast<uint32_t>(max_elements), out, workspace, workspace_bytes,
-                        stream);
+  return scatter_pooled_common(emb_rows, dim, inverse, slots, pad_index, grad, batch, features, max_elements,
+                               out, FLARE_FLOAT32, workspace, workspace_bytes, stream);
+}
+
+extern "C" int flare_scatter_pooled_ex(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                                       int64_t slots, int32_t pad_index, const float *grad,
+                                       int64_t batch, int32_t features, int32_t max_elements,
+                                       void *out, int32_t out_dtype, void *workspace,
+                                       size_t workspace_bytes, void *stream) {
+  return scatter_pooled_common(emb_rows, dim, inverse, slots, pad_index, grad, batch, features, max_elements,
+                               out, out_dtype, workspace, workspace_bytes, stream);
 }
 
 // ----------------------------------------------------------------------------
@@ -2062,9 +2107,10 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     Workspace w = layout_workspace(workspace, n, 4, 1, false, false, false);
     const RadixPlan plan = radix_plan(bits, 4);
     FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
-    prepare_generic_kernel<SrcT, uint32_t><<<grid, 256, 0, s>>>(values, n, minimum, plan.passes,
+    prepare_generic_kernel<SrcT, uint32_t><<<grid, 256, 0, s>>>(values, n, minimum,
+                                                                static_cast<uint64_t>(key_bound), plan.passes,
                                                                 plan.digit_bits,
-                                                                static_cast<uint32_t *>(w.keys[0]), w.hist);
+                                                                static_cast<uint32_t *>(w.keys[0]), w.hist, err);
     FLARE_TRY_HIP(hipGetLastError());
     int sorted = 0;
     FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, &sorted));
@@ -2081,9 +2127,10 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
   Workspace w = w8;
   const RadixPlan plan = radix_plan(bits, 8);
   FLARE_TRY(launch_zero(workspace, zero_bytes_for(w, plan), s));
-  prepare_generic_kernel<SrcT, uint64_t><<<grid, 256, 0, s>>>(values, n, minimum, plan.passes,
+  prepare_generic_kernel<SrcT, uint64_t><<<grid, 256, 0, s>>>(values, n, minimum,
+                                                              static_cast<uint64_t>(key_bound), plan.passes,
                                                               plan.digit_bits,
-                                                              static_cast<uint64_t *>(w.keys[0]), w.hist);
+                                                              static_cast<uint64_t *>(w.keys[0]), w.hist, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   FLARE_TRY(run_sort<uint64_t>(w, plan, err, s, &sorted));

@@ -34,20 +34,24 @@ def unique_global_flat_positions(nested_splits: Sequence[Any], flat_first_indice
         )
     host_result = isinstance(flat_first_indices, np.ndarray)
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    lib = _native.library()
-    splits = [contiguous(to_device(s, dev).reshape(-1).to(torch.int64)) for s in nested_splits]
-    first = contiguous(to_device(flat_first_indices, dev).reshape(-1).to(torch.int64))
-    origin = contiguous(to_device(origin_indices, dev).reshape(-1).to(torch.int64))
-    out = torch.empty(max(int(first.numel()), 1), dtype=torch.int32, device=dev)
-    levels = len(splits)
-    ptrs = (ctypes.c_void_p * levels)(*[s.data_ptr() for s in splits])
-    lengths = (ctypes.c_int64 * levels)(*[int(s.numel()) for s in splits])
-    dims = (ctypes.c_int64 * levels)(*[int(w) for w in widths])
+    _native.library()
     s = torch.cuda.current_stream(dev) if stream is None else stream
-    _native.call("flare_nested_global_positions", first.data_ptr(), int(first.numel()), levels,
-                 ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(lengths, ctypes.c_void_p),
-                 origin.data_ptr(), int(origin.numel()), ctypes.cast(dims, ctypes.c_void_p), out.data_ptr(),
-                 int(s.cuda_stream))
+    caller = torch.cuda.current_stream(dev)
+    if s != caller:
+        s.wait_stream(caller)  # device inputs the caller's stream is still producing
+    with torch.cuda.stream(s):  # the conversions and the kernel on one stream, in order
+        splits = [contiguous(to_device(sp, dev).reshape(-1).to(torch.int64)) for sp in nested_splits]
+        first = contiguous(to_device(flat_first_indices, dev).reshape(-1).to(torch.int64))
+        origin = contiguous(to_device(origin_indices, dev).reshape(-1).to(torch.int64))
+        out = torch.empty(max(int(first.numel()), 1), dtype=torch.int32, device=dev)
+        levels = len(splits)
+        ptrs = (ctypes.c_void_p * levels)(*[sp.data_ptr() for sp in splits])
+        lengths = (ctypes.c_int64 * levels)(*[int(sp.numel()) for sp in splits])
+        dims = (ctypes.c_int64 * levels)(*[int(w) for w in widths])
+        _native.call("flare_nested_global_positions", first.data_ptr(), int(first.numel()), levels,
+                     ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(lengths, ctypes.c_void_p),
+                     origin.data_ptr(), int(origin.numel()), ctypes.cast(dims, ctypes.c_void_p), out.data_ptr(),
+                     int(s.cuda_stream))
     result = out[: int(first.numel())]
     s.synchronize()
     if result.numel() and bool((result < 0).any()):

@@ -190,28 +190,43 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
             return DeviceArray(output)
 
     # ------------------------------------------------------------------ backward
+    def _out_dtype(self, out_dtype: Any) -> torch.dtype:
+        """Keyed-sum output dtype: the gradient dtype (float32), or the bfloat16 transport
+        dtype, rounded as the sums are stored (the caller's grad.astype(transport),
+        train_worker.py:518-522, fused into the scatter)."""
+        if out_dtype is None:
+            return torch.float32
+        name = out_dtype if isinstance(out_dtype, str) else getattr(out_dtype, "name", str(out_dtype))
+        if name in ("float32", "torch.float32"):
+            return torch.float32
+        if name in ("bfloat16", "torch.bfloat16"):
+            return torch.bfloat16
+        raise TypeError(f"scatter output dtype must be float32 or bfloat16, got {out_dtype!r}")
+
     def scatter(self, emb_rows: int, emb_dim: int, inverse: Any, pad_index: int,
-                gradient: Any) -> DeviceArray:
+                gradient: Any, *, out_dtype: Any = None) -> DeviceArray:
         with self.stream:
             inverse = contiguous(self._inverse_on_stream(inverse).reshape(-1))
             gradient = contiguous(
                 self._array_on_stream(gradient).to(torch.float32).reshape(-1, emb_dim)
             )
-            output = torch.empty((emb_rows, emb_dim), dtype=torch.float32, device=self.device)
+            out_t = self._out_dtype(out_dtype)
+            output = torch.empty((emb_rows, emb_dim), dtype=out_t, device=self.device)
             slots = int(inverse.numel())
             if gradient.shape[0] != slots:
                 raise ValueError("scatter gradient rows must match inverse slots")
             nbytes = _native.library().flare_scatter_workspace_bytes(slots, emb_rows, emb_dim)
             workspace = self._workspace(nbytes)
             _native.call(
-                "flare_scatter", emb_rows, emb_dim, inverse.data_ptr(), slots, int(pad_index),
-                gradient.data_ptr(), output.data_ptr(), workspace.data_ptr(), nbytes,
+                "flare_scatter_ex", emb_rows, emb_dim, inverse.data_ptr(), slots, int(pad_index),
+                gradient.data_ptr(), output.data_ptr(), storage_code(out_t), workspace.data_ptr(), nbytes,
                 self.stream.ptr,
             )
             return DeviceArray(output)
 
     def scatter_pooled(self, emb_rows: int, emb_dim: int, inverse: Any, pad_index: int,
-                       gradient: Any, target_widths: SparsePooledWidths) -> DeviceArray:
+                       gradient: Any, target_widths: SparsePooledWidths, *,
+                       out_dtype: Any = None) -> DeviceArray:
         with self.stream:
             feature_count, max_elements = pooled_sparse_widths(target_widths)
             inverse = contiguous(self._inverse_on_stream(inverse).reshape(-1))
@@ -224,13 +239,15 @@ class HipSparseEmbeddingOperator(SparseEmbeddingOperator):
                 raise ValueError(
                     "pooled scatter inverse slots must match gradient rows times max_elements"
                 )
-            output = torch.empty((emb_rows, emb_dim), dtype=torch.float32, device=self.device)
+            out_t = self._out_dtype(out_dtype)
+            output = torch.empty((emb_rows, emb_dim), dtype=out_t, device=self.device)
             nbytes = _native.library().flare_scatter_workspace_bytes(slots, emb_rows, emb_dim)
             workspace = self._workspace(nbytes)
             _native.call(
-                "flare_scatter_pooled", emb_rows, emb_dim, inverse.data_ptr(), slots,
+                "flare_scatter_pooled_ex", emb_rows, emb_dim, inverse.data_ptr(), slots,
                 int(pad_index), gradient.data_ptr(), pooled_slots // feature_count, feature_count,
-                max_elements, output.data_ptr(), workspace.data_ptr(), nbytes, self.stream.ptr,
+                max_elements, output.data_ptr(), storage_code(out_t), workspace.data_ptr(), nbytes,
+                self.stream.ptr,
             )
             return DeviceArray(output)
 

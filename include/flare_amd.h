@@ -161,6 +161,22 @@ int flare_scatter_pooled(int64_t emb_rows, int32_t dim, const int32_t *inverse,
                          float *out, void *workspace, size_t workspace_bytes,
                          void *stream);
 
+/* flare_scatter / flare_scatter_pooled with the keyed sums written in the
+ * gradient transport dtype: out_dtype FLARE_FLOAT32, or FLARE_BFLOAT16 (the
+ * fp32 sums rounded to nearest even as each row is stored).  This fuses the
+ * cast the caller runs after scatter_pooled, grad.astype(transport)
+ * (recipes/recsys/ranking/workers/train_worker.py:518-522; the CuPy backend's
+ * astype, gpu_cupy.py:434,474): out is [emb_rows, dim] of out_dtype. */
+int flare_scatter_ex(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                     int64_t slots, int32_t pad_index, const float *grad,
+                     void *out, int32_t out_dtype, void *workspace,
+                     size_t workspace_bytes, void *stream);
+int flare_scatter_pooled_ex(int64_t emb_rows, int32_t dim, const int32_t *inverse,
+                            int64_t slots, int32_t pad_index, const float *grad,
+                            int64_t batch, int32_t features, int32_t max_elements,
+                            void *out, int32_t out_dtype, void *workspace,
+                            size_t workspace_bytes, void *stream);
+
 size_t flare_unique_workspace_bytes(int64_t n, int32_t key_dtype);
 
 /* unique_first_occurrence (src/flare/ops/sparse_unique.py:52-77) and the GPU
@@ -168,7 +184,8 @@ size_t flare_unique_workspace_bytes(int64_t n, int32_t key_dtype);
  * unique keys in first-occurrence order, inverse (int32) and first_indices
  * (int64).  values: [n] of key_dtype (int32/uint32/int64/uint64).
  * unique_out must hold n keys; *unique_count (device int64) receives U.
- * key_bound > 0 promises 0 <= key < key_bound (no synchronization); with
+ * key_bound > 0 promises 0 <= key < key_bound (no synchronization; a key
+ * outside it sets device error bit 1 and the results are not defined); with
  * key_bound == 0 the call reads the key range back to the host (synchronizes
  * the stream once). */
 int flare_unique_first_occurrence(const void *values, int32_t key_dtype,

@@ -129,3 +129,16 @@ def test_more_tiles_than_the_fused_prefix_covers(gpu_device, no_device_errors, d
     np.testing.assert_array_equal(first.cpu().numpy(), first_idx[order])
     np.testing.assert_array_equal(inverse.cpu().numpy(), rank_of_sorted[inv_sorted.reshape(-1)])
     no_device_errors()
+
+
+@pytest.mark.parametrize("bad", [-1, 50, 1 << 40])
+def test_key_bound_violation_sets_the_error_bit(gpu_device, no_device_errors, bad):
+    """key_bound promises 0 <= key < key_bound; a key outside it is reported (device error bit 1)
+    instead of silently splitting its run."""
+    from flare_amd.unique import unique_first_occurrence
+
+    keys = torch.tensor([3, 7, bad, 3, 9], dtype=torch.int64, device=gpu_device)
+    unique_first_occurrence(keys, key_bound=50)
+    no_device_errors(1)
+    unique_first_occurrence(torch.tensor([3, 7, 49, 3], dtype=torch.int64, device=gpu_device), key_bound=50)
+    no_device_errors(0)
