@@ -1,9 +1,9 @@
-// Thread-local error messages and the per-device error word.
+// Thread-local error messages and reading back the per-device error word
+// (device_word.hip holds the word itself).
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
 #include <cstdio>
-#include <mutex>
 
 #include "common.hpp"
 
@@ -11,8 +11,6 @@ namespace flare {
 
 namespace {
 thread_local char g_message[512] = "";
-std::mutex g_word_mutex;
-int *g_words[64] = {};
 }  // namespace
 
 int fail(int code, const char *fmt, ...) {
@@ -25,28 +23,6 @@ int fail(int code, const char *fmt, ...) {
 
 int hip_fail(hipError_t err, const char *what) {
   return fail(FLARE_ERR_HIP, "%s failed: %s", what, hipGetErrorString(err));
-}
-
-int *device_error_word(int *status) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= 64) {
-    *status = hip_fail(e == hipSuccess ? hipErrorInvalidDevice : e, "hipGetDevice");
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(g_word_mutex);
-  if (!g_words[dev]) {
-    int *p = nullptr;
-    e = hipMalloc(&p, sizeof(int));
-    if (e == hipSuccess) e = hipMemset(p, 0, sizeof(int));
-    if (e != hipSuccess) {
-      *status = hip_fail(e, "allocating the device error word");
-      return nullptr;
-    }
-    g_words[dev] = p;
-  }
-  *status = FLARE_OK;
-  return g_words[dev];
 }
 
 }  // namespace flare
