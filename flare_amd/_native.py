@@ -61,6 +61,7 @@ SIGNATURES = {
     "flare_scatter_pooled_ex": (_i32, [_i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i32, _vp, _sz, _vp]),
     "flare_unique_workspace_bytes": (_sz, [_i64, _i32]),
     "flare_unique_first_occurrence": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "flare_unique_first_occurrence_noalloc": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "flare_sparse_update_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "flare_sparse_update": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, ctypes.POINTER(FlareOptimizer), _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
     "flare_pooled_backward_workspace_bytes": (_sz, [_i64, _i64, _i32]),

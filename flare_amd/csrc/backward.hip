@@ -22,6 +22,8 @@
 //               (or the reduced gradient) written once per unique key
 #include "backward.hpp"
 
+#include <mutex>
+
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -2166,6 +2168,57 @@ extern "C" int flare_unique_first_occurrence(const void *values, int32_t key_dty
     case FLARE_UINT64: return unique_typed(static_cast<const uint64_t *>(values), n, key_bound, unique_out, inverse_out, first_indices_out, unique_count, workspace, workspace_bytes, s);
     default: return fail(FLARE_ERR_DTYPE, "sparse unique requires integer keys, got dtype code %d", key_dtype);
   }
+}
+
+// ----------------------------------------------------------------------------
+// unique_first_occurrence without allocating: the workspace is `scratch`, a
+// fixed array every GPU holds from the moment the code object loads until the
+// process ends.  Host code uses the address hipGetSymbolAddress returns for
+// the current device (kept per device), never the array's name: in host code
+// that name is only a stand-in for the symbol, not a device address.
+// ----------------------------------------------------------------------------
+namespace flare {
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t{48} << 20;  // 2^20 keys of any dtype fit
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mutex;
+void *g_scratch[64] = {};
+
+// The current device's scratch address, looked up once per device (with it current).
+int scratch_address(void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64)
+    return hip_fail(e == hipSuccess ? hipErrorInvalidDevice : e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return hip_fail(e == hipSuccess ? hipErrorInvalidSymbol : e, "hipGetSymbolAddress(scratch)");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return FLARE_OK;
+}
+}  // namespace
+}  // namespace flare
+
+extern "C" int flare_unique_first_occurrence_noalloc(const void *values, int32_t key_dtype, int64_t n,
+                                                     int64_t key_bound, void *unique_out, int32_t *inverse_out,
+                                                     int64_t *first_indices_out, int64_t *unique_count,
+                                                     void *stream) {
+  if (n < 0) return fail(FLARE_ERR_SHAPE, "negative key count");
+  if (key_bound <= 0)
+    return fail(FLARE_ERR_ARGUMENT, "the allocation-free unique needs key_bound > 0 (it reads nothing back to the host)");
+  const size_t need = flare_unique_workspace_bytes(n, key_dtype);
+  if (need > kNoAllocScratchBytes)
+    return fail(FLARE_ERR_LIMIT, "%lld keys need %zu bytes of workspace; the allocation-free unique holds %zu "
+                "(at most 1048576 keys)", static_cast<long long>(n), need, kNoAllocScratchBytes);
+  void *workspace = nullptr;
+  FLARE_TRY(scratch_address(&workspace));
+  return flare_unique_first_occurrence(values, key_dtype, n, key_bound, unique_out, inverse_out, first_indices_out,
+                                       unique_count, workspace, kNoAllocScratchBytes, stream);
 }
 
 // ----------------------------------------------------------------------------

@@ -195,6 +195,24 @@ int flare_unique_first_occurrence(const void *values, int32_t key_dtype,
                                   int64_t *unique_count, void *workspace,
                                   size_t workspace_bytes, void *stream);
 
+/* flare_unique_first_occurrence without a workspace argument and without
+ * allocating: no counterpart in the reference; for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  The workspace is a fixed scratch array
+ * of 48 MiB that every GPU the library runs on holds until the process ends:
+ * n up to 1048576 keys of any key dtype (a larger n whose workspace would not
+ * fit returns FLARE_ERR_LIMIT).  key_bound > 0 is required (nothing is read
+ * back to the host, nothing synchronizes).  Every call on one GPU shares that
+ * GPU's array, which keeps the last call's contents (each call clears what
+ * must start at zero), so calls that overlap on one GPU (two streams, two
+ * threads) race: order them on one stream.  Outputs as
+ * flare_unique_first_occurrence. */
+int flare_unique_first_occurrence_noalloc(const void *values, int32_t key_dtype,
+                                          int64_t n, int64_t key_bound,
+                                          void *unique_out, int32_t *inverse_out,
+                                          int64_t *first_indices_out,
+                                          int64_t *unique_count, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Sparse optimizer update on a dense, row-indexed table shard in HBM.
  *
