@@ -113,19 +113,19 @@ def update_kernel_bytes(w, s: int) -> tuple[int, int]:
 
 
 def kernel_traffic(config: int, kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed counter runs, or None.
+    """HBM bytes per launch of ``kernel`` on workload ``config`` from the committed counter runs.
 
-    profiles/step_kernel_traffic.json holds FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch) of the step's kernels on one workload and the factors that map
-    each counter onto the bytes of a plain device copy of known size.
+    profiles/step_kernel_traffic.json holds, per workload, FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch) of the step's kernels and the factors that map each counter onto the bytes of a
+    plain device copy of known size.  None when the workload or kernel was not profiled.
     """
     path = ROOT / "profiles" / "step_kernel_traffic.json"
     if not path.exists():
         return None
-    rec = json.loads(path.read_text())
-    k = rec.get("kernels", {}).get(kernel)
-    if rec.get("workload_id") != config or k is None:
+    rec = json.loads(path.read_text()).get("workloads", {}).get(str(config))
+    if rec is None or kernel not in rec.get("kernels", {}):
         return None
+    k = rec["kernels"][kernel]
     return (k["fetch_kib"] * rec["fetch_scale"] + k["write_kib"] * rec["write_scale"]) * 1024.0
 
 
@@ -582,6 +582,51 @@ def row_gather_main(args) -> int:
     return 0
 
 
+def ceiling_main(args) -> int:
+    """What plain streaming kernels reach on this GPU over 1 GiB: the ceiling the step's
+    kernels are measured against.
+
+    write: ``flare_zero_bytes`` (16-byte stores); copy: ``flare_copy_rows`` of one contiguous
+    block (16-byte loads and stores, reported as bytes read + written); read:
+    ``flare_check_finite`` over 1 GiB of float32 (16-byte loads, one flag written); and
+    PyTorch's own ``copy_`` and ``sum`` beside them.  Each is the median of ``--steps`` calls
+    timed with events.
+    """
+    import torch
+
+    from flare_amd import _native
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    stream = torch.cuda.Stream(device)
+    nbytes = 1 << 30
+    with torch.cuda.stream(stream):
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device=device).uniform_()
+        dst = torch.empty_like(src)
+        flag = torch.empty(1, dtype=torch.int32, device=device)
+    s = int(stream.cuda_stream)
+    cases = [
+        ("write", nbytes, lambda: _native.call("flare_zero_bytes", dst.data_ptr(), nbytes, s)),
+        ("copy", 2 * nbytes, lambda: _native.call("flare_copy_rows", src.data_ptr(), nbytes // 4096, dst.data_ptr(),
+                                                  nbytes // 4096, 4096, None, None, nbytes // 4096, s)),
+        ("read", nbytes, lambda: _native.call("flare_check_finite", src.data_ptr(), _native.FLOAT32, nbytes // 4,
+                                              flag.data_ptr(), s)),
+        ("torch copy_", 2 * nbytes, lambda: dst.copy_(src)),
+        ("torch sum", nbytes, lambda: src.sum()),
+    ]
+    for name, moved, fn in cases:
+        with torch.cuda.stream(stream):
+            ms = _event_ms(stream, fn, args.steps, args.warmup)
+        gbs = moved / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": f"1 GiB {name} GB/s", "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_call": ms, "higher_is_better": True, "dtype": "raw bytes",
+            "data": "synthetic (uniform fp32)", "config": {"workload": f"{name} of 1 GiB"},
+            "fraction_of_peak": gbs / PEAK_HBM_GBS,
+        }), flush=True)
+    return 0
+
+
 def keymap_main(args) -> int:
     """Dynamic store: lookup_or_insert of one step's unique keys into a 128-wide bf16 table.
 
@@ -680,6 +725,8 @@ def main() -> int:
                     help="measure CSR-native ingest (nested global positions) instead of the pooled step")
     ap.add_argument("--row-gather", action="store_true",
                     help="measure this GPU's random-row gather rate (the update's gradient gather ceiling)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="measure this GPU's streaming ceilings (1 GiB write, copy, read) instead of the pooled step")
     ap.add_argument("--pages", action="store_true",
                     help="measure checkpoint page image export/import instead of the pooled step")
     args = ap.parse_args()
@@ -697,6 +744,8 @@ def main() -> int:
         return pages_main(args)
     if args.row_gather:
         return row_gather_main(args)
+    if args.ceiling:
+        return ceiling_main(args)
 
     import torch
 

@@ -914,7 +914,7 @@ struct UpdateArgs {
   float *s1;
   int32_t *step;
   float lr, eps, b1, b2, omb1, omb2;
-  double b1d, b2d;
+  double ln_b1, ln_b2;  // natural logs of the Adam betas (bias corrections 1 - beta^step)
   uint32_t units;
   uint32_t n;
   int *err;
@@ -1022,8 +1022,11 @@ __device__ __forceinline__ void apply_update(const UpdateArgs &a, uint32_t key, 
       }
     } else {  // Adam: m, v and the row are loaded here (too many registers to load ahead)
       const int32_t st = a.step[row] + 1;
-      const float bc1 = static_cast<float>(1.0 - pow(a.b1d, static_cast<double>(st)));
-      const float bc2 = static_cast<float>(1.0 - pow(a.b2d, static_cast<double>(st)));
+      // beta^step as exp(step * ln beta) in double, ln beta from the host: a few
+      // double ulps from pow, so the same bias corrections once rounded to float,
+      // at a quarter of pow's cost (on 1.1M rows of 128: 643 against 849 us)
+      const float bc1 = static_cast<float>(1.0 - exp(static_cast<double>(st) * a.ln_b1));
+      const float bc2 = static_cast<float>(1.0 - exp(static_cast<double>(st) * a.ln_b2));
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = (c * G + lane) * VEC;
@@ -1900,8 +1903,8 @@ void fill_optimizer(UpdateArgs &a, const flare_optimizer *opt) {
   a.b2 = static_cast<float>(opt->beta2);
   a.omb1 = static_cast<float>(1.0 - opt->beta1);
   a.omb2 = static_cast<float>(1.0 - opt->beta2);
-  a.b1d = opt->beta1;
-  a.b2d = opt->beta2;
+  a.ln_b1 = std::log(opt->beta1);
+  a.ln_b2 = std::log(opt->beta2);
 }
 
 int check_state(int mode, float *s0, float *s1, int32_t *step) {

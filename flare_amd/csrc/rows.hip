@@ -41,6 +41,18 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(U *__restrict__ dst
     dst[t] = U{};
 }
 
+// Contiguous copy of `units` U-sized units: one unit per thread over a full
+// grid of short blocks.  At any moment the blocks in flight cover one compact
+// window of the source and the destination, which keeps HBM streaming; the
+// same copy written as a grid-stride loop over a capped grid moved 10-25%
+// less on this GPU (blocks drift apart and spread over many DRAM pages).
+template <typename U>
+__global__ __launch_bounds__(kThreads) void copy_contiguous_kernel(const U *__restrict__ src, U *__restrict__ dst,
+                                                                   int64_t units) {
+  const int64_t t = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+  if (t < units) dst[t] = src[t];
+}
+
 // dst[i] = src[i] converted through float32 (exact widening, round-to-nearest-
 // even narrowing); four elements per thread.
 template <typename SrcTag, typename DstTag>
@@ -108,7 +120,8 @@ extern "C" int flare_zero_bytes(void *dst, int64_t bytes, void *stream) {
     }
   }
   const int64_t units = bytes / unit;
-  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(units, kThreads), 1 << 16));
+  // one unit per thread (a full grid of short blocks) up to 2^31 - 1 blocks
+  const int grid = static_cast<int>(std::min<int64_t>(ceil_div(units, kThreads), 0x7fffffff));
   if (unit == 16) fill_zero_kernel<uint4><<<grid, kThreads, 0, s>>>(static_cast<uint4 *>(dst), units);
   else if (unit == 4) fill_zero_kernel<uint32_t><<<grid, kThreads, 0, s>>>(static_cast<uint32_t *>(dst), units);
   else fill_zero_kernel<uint8_t><<<grid, kThreads, 0, s>>>(static_cast<uint8_t *>(dst), units);
@@ -137,6 +150,24 @@ extern "C" int flare_copy_rows(const void *src, int64_t src_rows, void *dst, int
     }
   }
   const int64_t units = row_bytes / unit;
+  if (!src_index && !dst_index && ceil_div(n * units, kThreads) <= 0x7fffffff) {
+    // rows 0 .. n-1 onto rows 0 .. n-1: one contiguous block of n * row_bytes bytes
+    const int cgrid = static_cast<int>(ceil_div(n * units, kThreads));
+    switch (unit) {
+      case 16: copy_contiguous_kernel<uint4><<<cgrid, kThreads, 0, s>>>(static_cast<const uint4 *>(src),
+                                                                        static_cast<uint4 *>(dst), n * units); break;
+      case 8: copy_contiguous_kernel<uint2><<<cgrid, kThreads, 0, s>>>(static_cast<const uint2 *>(src),
+                                                                       static_cast<uint2 *>(dst), n * units); break;
+      case 4: copy_contiguous_kernel<uint32_t><<<cgrid, kThreads, 0, s>>>(static_cast<const uint32_t *>(src),
+                                                                          static_cast<uint32_t *>(dst), n * units);
+        break;
+      default: copy_contiguous_kernel<uint16_t><<<cgrid, kThreads, 0, s>>>(static_cast<const uint16_t *>(src),
+                                                                           static_cast<uint16_t *>(dst), n * units);
+        break;
+    }
+    FLARE_TRY_HIP(hipGetLastError());
+    return FLARE_OK;
+  }
   const int grid = static_cast<int>(std::min<int64_t>(ceil_div(n * units, kThreads), 1 << 16));
   switch (unit) {
     case 16:
