@@ -1,0 +1,12 @@
+// Update kernels instantiated for optimizer updates of float32 tables.
+#include "update.hpp"
+
+namespace flare {
+
+int launch_update_f32(int mode, const UpdateArgs &a, const Shape &sh, hipStream_t s) {
+  if (mode == kModeSgd) return launch_update_tag<TagF32, kModeSgd>(a, sh, s);
+  if (mode == kModeAdam) return launch_update_tag<TagF32, kModeAdam>(a, sh, s);
+  return launch_update_tag<TagF32, kModeAdagrad>(a, sh, s);
+}
+
+}  // namespace flare
