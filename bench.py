@@ -51,14 +51,15 @@ def log(msg: str) -> None:
 
 
 def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weighted: bool,
-               optimizer: str) -> tuple[int, int, int]:
+               optimizer: str, g: int = 4) -> tuple[int, int, int]:
     """Algorithmic HBM bytes (forward, backward, update kernel) of one step.
 
     forward : ids N*8 + offsets T*(B+1)*4 + weights N*4 + unique rows U*D*s + pooled B*T*D*s
-    backward: ids N*8 + offsets + weights + fp32 pooled grads B*T*D*4 + unique U*8 + inverse N*4
+    backward: ids N*8 + offsets + weights + pooled grads B*T*D*g + unique U*8 + inverse N*4
               + rows 2*U*D*s + state 2*U*S   (S = 4 row-wise Adagrad, 2*D*4+4 Adam)
               (gradient-only: U*D*4 reduced gradients instead of rows and state)
-    update kernel: grads B*T*D*4 + rows 2*U*D*s + state 2*U*S + inverse N*4
+    update kernel: grads B*T*D*g + rows 2*U*D*s + state 2*U*S + inverse N*4
+    (g: bytes of a pooled gradient element, 4 for float32, 2 for the bfloat16 transport dtype)
     """
     offsets = tables * (batch + 1) * 4
     w = n * 4 if weighted else 0
@@ -68,12 +69,12 @@ def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weight
     else:
         state = 2 * dim * 4 + 4 if optimizer == "adam" else STATE_BYTES[optimizer]
         rows_state = 2 * u * dim * s + 2 * u * state
-    bwd = n * 8 + offsets + w + batch * tables * dim * 4 + u * 8 + n * 4 + rows_state
-    update = batch * tables * dim * 4 + rows_state + n * 4
+    bwd = n * 8 + offsets + w + batch * tables * dim * g + u * 8 + n * 4 + rows_state
+    update = batch * tables * dim * g + rows_state + n * 4
     return fwd, bwd, update
 
 
-def update_kernel_bytes(w, s: int) -> tuple[int, int]:
+def update_kernel_bytes(w, s: int, g: int = 4) -> tuple[int, int]:
     """Algorithmic HBM bytes of the two update kernels for one batch ``w``.
 
     Keys are stably sorted; a key is "long" when its sorted positions cross a 64-position
@@ -81,9 +82,10 @@ def update_kernel_bytes(w, s: int) -> tuple[int, int]:
     unit piece), else "short" (summed inside apply_kernel).  A bag's gradient row is read once
     per kernel however many of its occurrences that kernel sums (R_long, R_short: distinct
     bags among the long and the short occurrences).
-    sums_kernel : R_long * D*4 gradient rows + N_long * 4 row indices + P_long * D*4 partials
-    apply_kernel: U * (2*D*s row read and write + 2*S state) + R_short * D*4 + N_short * 4
+    sums_kernel : R_long * D*g gradient rows + N_long * 4 row indices + P_long * D*4 partials
+    apply_kernel: U * (2*D*s row read and write + 2*S state) + R_short * D*g + N_short * 4
                   + U_long * D*4 (the long key's folded sum)
+    (g: bytes of a pooled gradient element)
     """
     import numpy as np
 
@@ -107,8 +109,8 @@ def update_kernel_bytes(w, s: int) -> tuple[int, int]:
     else:
         state = 2 * dim * 4 + 4 if w.optimizer == "adam" else STATE_BYTES[w.optimizer]
         rows_state = 2 * u * dim * s + 2 * u * state
-    sums = r_long * dim * 4 + n_long * 4 + p_long * dim * 4
-    apply = rows_state + r_short * dim * 4 + n_short * 4 + u_long * dim * 4
+    sums = r_long * dim * g + n_long * 4 + p_long * dim * 4
+    apply = rows_state + r_short * dim * g + n_short * 4 + u_long * dim * 4
     return sums, apply
 
 
@@ -717,6 +719,11 @@ def main() -> int:
                          "(a kernel of known traffic, to scale FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--layout", choices=["table_major", "sample_major"], default="table_major",
                     help="pooled row layout: [T, B, D] (the T per-table outputs one after the other) or [B, T, D]")
+    ap.add_argument("--grad-dtype", choices=["auto", "float32", "bfloat16"], default="auto",
+                    help="dtype of the pooled gradient handed to the update. auto: bfloat16 for bf16/fp16 "
+                         "tables (the gradient transport dtype of the reference's BF16 and FP16 precision "
+                         "policies, src/flare/jax/training/precision.py:62-69, cast before the gradient "
+                         "leaves the JAX worker, train_worker.py:467-474), float32 for float32 tables")
     ap.add_argument("--overlap", action="store_true",
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
@@ -769,9 +776,15 @@ def main() -> int:
              for b in batches]
     gen = torch.Generator(device=device)
     gen.manual_seed(2)
+    grad_dtype = args.grad_dtype
+    if grad_dtype == "auto":
+        grad_dtype = "float32" if w0.value_dtype == "float32" else "bfloat16"
+    g_bytes = 4 if grad_dtype == "float32" else 2
     with torch.cuda.stream(shard.stream):
         grad = torch.randn(shard.pooled_shape(w0.batch), generator=gen, device=device,
                            dtype=torch.float32).mul_(1e-3)
+        if grad_dtype == "bfloat16":
+            grad = grad.to(torch.bfloat16)  # round to nearest even, as the transport cast
         grad_out = None
         none_opt = None
         if w0.optimizer == "none":
@@ -870,7 +883,7 @@ def main() -> int:
         log(f"full-size check: {check}")
     check["passed"] = bool(timed_errors == 0 and check.get("passed", True))
 
-    kernel_bytes = [update_kernel_bytes(b, s) for b in batches]
+    kernel_bytes = [update_kernel_bytes(b, s, g_bytes) for b in batches]
     step_ms, fwd_ms, dedup_ms, apply_ms = [], [], [], []
     step_gbs, fwd_gbs, upd_gbs = [], [], []
     sums_ms, fold_ms, applyk_ms, sums_gbs, applyk_gbs = [], [], [], [], []
@@ -884,7 +897,7 @@ def main() -> int:
         dedup_ms.append(ev[2].elapsed_time(ev[3]))
         apply_ms.append(a)
         fb, bb, ub = step_bytes(b.num_ids, uniques[order[i]], b.batch, b.num_tables, b.dim, s,
-                                b.weights is not None, b.optimizer)
+                                b.weights is not None, b.optimizer, g_bytes)
         step_gbs.append((fb + bb) / (t * 1e-3) / 1e9)
         fwd_gbs.append(fb / (f * 1e-3) / 1e9)
         upd_gbs.append(ub / (a * 1e-3) / 1e9)
@@ -900,7 +913,7 @@ def main() -> int:
     rows = w0.batch * w0.num_tables
     achieved_step = statistics.median(step_gbs)
     fb0, bb0, ub0 = step_bytes(w0.num_ids, uniques[0], w0.batch, w0.num_tables, w0.dim, s,
-                               w0.weights is not None, w0.optimizer)
+                               w0.weights is not None, w0.optimizer, g_bytes)
     sb0, ab0 = kernel_bytes[0]
 
     def roofline(kernel, what, gbs, ms, nbytes):
@@ -925,7 +938,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (bf16 rows)" if w0.value_dtype == "bfloat16" else f"f32 ({w0.value_dtype} rows)",
+        "dtype": f"f32 ({'bf16' if w0.value_dtype == 'bfloat16' else w0.value_dtype} rows, "
+                 f"{'bf16' if grad_dtype == 'bfloat16' else 'f32'} pooled grads)",
         "data": "synthetic (seeded Zipf ids, N(0,1e-3) pooled grads, U(-0.01,0.01) rows)",
         "config": {
             "workload": WORKLOAD_NAMES[config],
@@ -938,6 +952,7 @@ def main() -> int:
             "rotated_batches": len(plans),
             "dedup": "concurrent with the forward" if overlap else "after the forward, same stream",
             "pooled_layout": "[T, B, D]" if args.layout == "table_major" else "[B, T, D]",
+            "pooled_grad_dtype": grad_dtype,
         },
         "hbm_gbs": achieved_step,
         "hbm_frac": achieved_step / PEAK_HBM_GBS,

@@ -1073,8 +1073,10 @@ int reduce_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, in
   a.err = err;
   const bool v4 = vec4_ok(grad) && (out ? vec4_ok(out) : true) && (table ? aligned(table, 8) : true) &&
                   (mode == kModeAdam ? (vec4_ok(s0) && vec4_ok(s1)) : true) && vec4_ok(w.partial);
+  // 16-byte lanes for bfloat16 gradients (every vector then 16-byte aligned)
+  const bool v8 = v4 && a.grad_bf16 && (table ? aligned(table, 16) : true);
   Shape sh;
-  FLARE_TRY(choose_shape(dim, v4, &sh));
+  FLARE_TRY(choose_shape(dim, v4, &sh, v8));
   return launch_update(mode, dtype, a, sh, s);
 }
 
@@ -1579,8 +1581,9 @@ extern "C" int flare_pooled_apply_ex(void *table, int32_t value_dtype, int64_t r
   const bool v4 = vec4_ok(pooled_grad) && (grad_out ? vec4_ok(grad_out) : true) &&
                   aligned(table, 8) && (mode == kModeAdam ? (vec4_ok(state0) && vec4_ok(state1)) : true) &&
                   vec4_ok(w.partial);
+  const bool v8 = v4 && a.grad_bf16 && aligned(table, 16);
   Shape sh;
-  FLARE_TRY(choose_shape(dim, v4, &sh));
+  FLARE_TRY(choose_shape(dim, v4, &sh, v8));
   return launch_update(mode, value_dtype, a, sh, s);
 }
 

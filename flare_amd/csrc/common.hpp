@@ -88,6 +88,11 @@ struct TagBF16 {
 
 // Raw vector of N bytes used for wide loads / stores.
 template <int N> struct Raw;
+// 32 bytes: two 16-byte halves (eight float32 lanes of one 16-byte-lane row slice)
+struct alignas(16) Bytes32 {
+  uint4 lo, hi;
+};
+template <> struct Raw<32> { using type = Bytes32; };
 template <> struct Raw<16> { using type = uint4; };
 template <> struct Raw<8> { using type = uint2; };
 template <> struct Raw<4> { using type = uint32_t; };

@@ -120,6 +120,37 @@ def test_multi_microstep_update_matches_oracle(gpu_device, no_device_errors, opt
     no_device_errors()
 
 
+@pytest.mark.parametrize("dim", [16, 64, 128])
+@pytest.mark.parametrize("count,repeat", [(300, 1), (700, 1), (65, 1), (4097, 1), (700, 3)])
+def test_every_key_updated_once_for_any_key_count(gpu_device, no_device_errors, dim, count, repeat):
+    """Key counts that split unevenly over the lane groups of a wave (single-occurrence keys
+    and, with repeat 3, keys of several occurrences): every touched row equals the oracle's
+    one row-wise Adagrad step, every other row is unchanged."""
+    from flare_amd.store import RowWiseAdagrad
+
+    rows = 8192
+    store = _store(capacity=rows, dims=[dim], value_dtype="float32", optimizer=RowWiseAdagrad(lr=0.01), seed=3)
+    table0 = store.tables[dim].table.cpu().numpy().copy()
+    rng = np.random.default_rng(count * 7 + dim + repeat)
+    distinct = rng.permutation(rows)[:count].astype(np.int64)
+    keys = np.concatenate([distinct] * repeat)
+    grad = rng.standard_normal((keys.size, dim), dtype=np.float32)
+    store.accumulate_gradients(keys, grad)
+    store.optimizer_step(1)
+    store.synchronize()
+    perm, sk, starts = O.sorted_occurrences(keys)
+    sums = O.segment_sums(grad[perm], starts, perm.size)
+    touched = sk[starts]
+    w2, acc2 = O.rowwise_adagrad_update(table0[touched], np.zeros(touched.size, np.float32), sums, lr=0.01)
+    got = store.tables[dim].table.cpu().numpy()
+    ulps = O.storage_ulp_distance(got[touched], w2, "float32")
+    assert ulps.max() <= 1, f"max ulp distance {ulps.max()}"
+    np.testing.assert_allclose(store.tables[dim].state0.cpu().numpy()[touched], acc2, rtol=1e-5)
+    untouched = np.setdiff1d(np.arange(rows), touched)
+    np.testing.assert_array_equal(got[untouched], table0[untouched])
+    no_device_errors()
+
+
 def test_rejects_bad_normalization_and_shapes(gpu_device):
     from flare_amd.store import Adam
 
