@@ -77,14 +77,19 @@ def step_bytes(n: int, u: int, batch: int, tables: int, dim: int, s: int, weight
 def update_kernel_bytes(w, s: int, g: int = 4) -> tuple[int, int]:
     """Algorithmic HBM bytes of the two update kernels for one batch ``w``.
 
-    Keys are stably sorted; a key is "long" when its sorted positions cross a 64-position
-    unit boundary or number more than 4 (those are summed by sums_kernel, one partial row per
-    unit piece), else "short" (summed inside apply_kernel).  A bag's gradient row is read once
-    per kernel however many of its occurrences that kernel sums (R_long, R_short: distinct
-    bags among the long and the short occurrences).
-    sums_kernel : R_long * D*g gradient rows + N_long * 4 row indices + P_long * D*4 partials
-    apply_kernel: U * (2*D*s row read and write + 2*S state) + R_short * D*g + N_short * 4
-                  + U_long * D*4 (the long key's folded sum)
+    Keys are stably sorted; a key's positions inside one 64-position unit form one piece.
+    A bag's gradient row is read once per kernel however many of that kernel's occurrences
+    it holds (R_x: distinct bags among the occurrences of kind x).
+
+    Optimizer updates (piece_sums_kernel, key_apply_kernel):
+    piece_sums: R_multi * D*g gradient rows of keys with several occurrences + N * 4 sorted
+                gradient rows + P_multi * D*4 piece rows written + N * 4 inverse
+    key_apply : U * (2*D*s row read and write + 2*S state) + R_single * D*g
+                + P_multi * D*4 piece rows read
+    Reduced gradients (sums_kernel, apply_kernel; "long" keys cross a unit boundary or have
+    more than 4 positions, the others are summed inside apply_kernel):
+    sums : R_long * D*g + N_long * 4 row indices + P_long * D*4 partials
+    apply: U * D*4 reduced rows written + R_short * D*g + N_short * 4 + U_long * D*4
     (g: bytes of a pooled gradient element)
     """
     import numpy as np
@@ -92,25 +97,29 @@ def update_kernel_bytes(w, s: int, g: int = 4) -> tuple[int, int]:
     keys = w.global_keys()
     dim = w.dim
     uniq, inverse, counts = np.unique(keys, return_inverse=True, return_counts=True)
+    n = int(counts.sum())
     starts = np.cumsum(counts) - counts
     h = starts // 64
     last = (starts + counts - 1) // 64
-    long_ = (h != last) | (counts > 4)
-    n_long = int(counts[long_].sum())
-    p_long = int((last - h + 1)[long_].sum())
-    u, u_long = int(counts.size), int(long_.sum())
-    n_short = int(counts.sum()) - n_long
+    pieces = last - h + 1
+    u = int(counts.size)
     bag = np.repeat(np.arange(w.num_tables * w.batch, dtype=np.int64), np.diff(w.offsets))
-    occ_long = long_[inverse.reshape(-1)]
-    r_long = int(np.unique(bag[occ_long]).size)
-    r_short = int(np.unique(bag[~occ_long]).size)
+    inverse = inverse.reshape(-1)
+
+    def bags_of(key_mask):
+        return int(np.unique(bag[key_mask[inverse]]).size)
+
     if w.optimizer == "none":
-        rows_state = u * dim * 4
-    else:
-        state = 2 * dim * 4 + 4 if w.optimizer == "adam" else STATE_BYTES[w.optimizer]
-        rows_state = 2 * u * dim * s + 2 * u * state
-    sums = r_long * dim * g + n_long * 4 + p_long * dim * 4
-    apply = rows_state + r_short * dim * g + n_short * 4 + u_long * dim * 4
+        long_ = (h != last) | (counts > 4)
+        n_long = int(counts[long_].sum())
+        sums = bags_of(long_) * dim * g + n_long * 4 + int(pieces[long_].sum()) * dim * 4
+        apply = u * dim * 4 + bags_of(~long_) * dim * g + (n - n_long) * 4 + int(long_.sum()) * dim * 4
+        return sums, apply
+    state = 2 * dim * 4 + 4 if w.optimizer == "adam" else STATE_BYTES[w.optimizer]
+    multi = counts > 1
+    p_multi = int(pieces[multi].sum())
+    sums = bags_of(multi) * dim * g + n * 4 + p_multi * dim * 4 + n * 4
+    apply = u * (2 * dim * s + 2 * state) + bags_of(~multi) * dim * g + p_multi * dim * 4
     return sums, apply
 
 
@@ -922,10 +931,15 @@ def main() -> int:
                 "traffic": kernel_traffic(config, kernel), "algorithmic_bytes_per_launch": nbytes,
                 "kernel_ms": statistics.median(ms)}
 
+    if w0.optimizer == "none":
+        sums_name = ("sums_kernel", "segment sums of long keys; one launch per step")
+        apply_name = ("apply_kernel", "short-key sums and the reduced gradients; one launch per step")
+    else:
+        sums_name = ("piece_sums_kernel", "per-piece sums of keys with several occurrences; one launch per step")
+        apply_name = ("key_apply_kernel", "row-wise update of every key; one launch per step")
     kernels = [roofline("pooled_kernel", "CSR pooled gather, forward; one launch per step", fwd_gbs, fwd_ms, fb0),
-               roofline("sums_kernel", "segment sums of long keys; one launch per step", sums_gbs, sums_ms, sb0),
-               roofline("apply_kernel", "short-key sums and row-wise update; one launch per step",
-                        applyk_gbs, applyk_ms, ab0)]
+               roofline(*sums_name, sums_gbs, sums_ms, sb0),
+               roofline(*apply_name, applyk_gbs, applyk_ms, ab0)]
     dominant = max(kernels, key=lambda k: k["kernel_ms"])
     result = {
         "metric": METRIC,

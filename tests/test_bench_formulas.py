@@ -18,27 +18,42 @@ def _workload(keys, offsets, batch, tables, dim, optimizer):
                            num_tables=tables, dim=dim, optimizer=optimizer)
 
 
-def test_long_short_and_unit_crossing_keys_one_id_per_bag():
-    # sorted positions: key 0 at 0..59 (60 > 4: long, one piece), key 1 at 60..61 (short),
-    # key 2 at 62..64 (crosses position 64: long, two pieces), key 3 at 65..66 and key 4 at
-    # 67..69 (short).  One id per bag, so every occurrence has its own gradient row.
-    keys = [0] * 60 + [1] * 2 + [2] * 3 + [3] * 2 + [4] * 3
+def test_pieces_singles_and_unit_crossing_keys_one_id_per_bag():
+    # sorted positions: key 0 at 0..59 (one piece), key 1 at 60..61, key 2 at 62..64 (crosses
+    # position 64: two pieces), key 3 at 65..66, key 4 at 67..69, key 5 once at 70 (single).
+    # One id per bag, so every occurrence has its own gradient row.
+    keys = [0] * 60 + [1] * 2 + [2] * 3 + [3] * 2 + [4] * 3 + [5]
     keys = np.random.default_rng(3).permutation(np.asarray(keys))  # order of occurrence is irrelevant
-    w = _workload(keys, np.arange(71), 70, 1, 4, "rowwise_adagrad")
+    w = _workload(keys, np.arange(72), 71, 1, 4, "rowwise_adagrad")
     sums, apply = bench.update_kernel_bytes(w, 2)
-    n_long, p_long, u, u_long, n_short = 63, 3, 5, 2, 7
-    assert sums == n_long * 4 * 4 + n_long * 4 + p_long * 4 * 4
+    n, n_multi, p_multi, u, n_single = 71, 70, 6, 6, 1
+    assert sums == n_multi * 4 * 4 + n * 4 + p_multi * 4 * 4 + n * 4
     rows_state = 2 * u * 4 * 2 + 2 * u * 4
-    assert apply == rows_state + n_short * 4 * 4 + n_short * 4 + u_long * 4 * 4
+    assert apply == rows_state + n_single * 4 * 4 + p_multi * 4 * 4
+    # bfloat16 pooled gradients: gradient rows at 2 bytes an element
+    sums2, apply2 = bench.update_kernel_bytes(w, 2, 2)
+    assert sums - sums2 == n_multi * 4 * 2 and apply - apply2 == n_single * 4 * 2
 
 
 def test_a_bag_row_counts_once_per_kernel():
-    # two bags of three ids: key 5 four times (short), keys 7 and 8 once; every occurrence is
-    # short, so sums reads nothing and apply reads each bag's gradient row once
+    # two bags of three ids: key 5 four times, keys 7 and 8 once each; piece_sums reads the two
+    # bags' rows once (key 5 occurs in both), key_apply the single keys' bag row once
     w = _workload([5, 5, 5, 5, 7, 8], [0, 3, 6], 2, 1, 4, "sgd")
     sums, apply = bench.update_kernel_bytes(w, 4)
-    assert sums == 0
-    assert apply == 2 * 3 * 4 * 4 + 2 * 4 * 4 + 6 * 4
+    assert sums == 2 * 4 * 4 + 6 * 4 + 1 * 4 * 4 + 6 * 4
+    assert apply == 3 * (2 * 4 * 4) + 1 * 4 * 4 + 1 * 4 * 4
+
+
+def test_reduced_gradient_kernels_long_and_short_keys():
+    # optimizer "none" (reduced gradients): sums_kernel takes keys crossing a unit boundary or
+    # of more than 4 positions, apply_kernel sums the others and writes U reduced rows
+    keys = [0] * 60 + [1] * 2 + [2] * 3 + [3] * 2 + [4] * 3
+    keys = np.random.default_rng(3).permutation(np.asarray(keys))
+    w = _workload(keys, np.arange(71), 70, 1, 4, "none")
+    sums, apply = bench.update_kernel_bytes(w, 2)
+    n_long, p_long, u, u_long, n_short = 63, 3, 5, 2, 7
+    assert sums == n_long * 4 * 4 + n_long * 4 + p_long * 4 * 4
+    assert apply == u * 4 * 4 + n_short * 4 * 4 + n_short * 4 + u_long * 4 * 4
 
 
 def test_step_bytes_follow_the_published_formula():
