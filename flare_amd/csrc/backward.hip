@@ -297,6 +297,9 @@ __global__ __launch_bounds__(256) void prepare_rows_kernel(const SrcT *__restric
 // gradients, the bag k itself for [T, B, D]) and, for mean pooling, the bag
 // length of every occurrence.
 constexpr int kPrepMaxBags = 4096;
+// Threads of a prepare block: about 512 blocks of 16 waves walk the bags, so
+// that each thread has few bags and the whole GPU has its loads in flight.
+constexpr int kPrepThreads = 1024;
 
 // Bags per prepare block: about 512 blocks (fewer histogram flushes), at most kPrepMaxBags bags each.
 constexpr int64_t kPerBagLength = 8;
@@ -310,7 +313,7 @@ int prep_bags_per_block(int64_t bags) {
 }
 
 template <typename IdT>
-__global__ __launch_bounds__(256) void prepare_csr_kernel(
+__global__ __launch_bounds__(kPrepThreads) void prepare_csr_kernel(
     const IdT *__restrict__ ids, int64_t n, const int64_t *__restrict__ offsets, int64_t bags,
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
@@ -318,10 +321,10 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     int table_major, int *err) {
   __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
-  for (int i = threadIdx.x; i < (passes << digit); i += 256) s_hist[i] = 0;
+  for (int i = threadIdx.x; i < (passes << digit); i += kPrepThreads) s_hist[i] = 0;
   const int64_t bag0 = static_cast<int64_t>(blockIdx.x) * bags_per_block;
   const int nb = static_cast<int>(std::min<int64_t>(bags_per_block, bags - bag0));
-  for (int i = threadIdx.x; i <= nb; i += 256) {
+  for (int i = threadIdx.x; i <= nb; i += kPrepThreads) {
     const int64_t o = offsets[bag0 + i];
     s_off[i] = o < 0 ? 0 : (o > n ? n : o);
     // offsets must start at 0, end at n and never decrease; otherwise some
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nb; i += 256)
+  for (int i = threadIdx.x; i < nb; i += kPrepThreads)
     if (s_off[i + 1] < s_off[i]) {
       record_error(err, kErrIndexOutOfRange);
       *reject = 1;
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     __shared__ int s_nlong;
     if (threadIdx.x == 0) s_nlong = 0;
     __syncthreads();
-    for (int lo = threadIdx.x; lo < nb; lo += 256) {
+    for (int lo = threadIdx.x; lo < nb; lo += kPrepThreads) {
       const int64_t b0 = s_off[lo], b1 = s_off[lo + 1];
       if (b1 - b0 > kPrepWalk) {
         const int slot = atomicAdd(&s_nlong, 1);
@@ -380,10 +383,10 @@ __global__ __launch_bounds__(256) void prepare_csr_kernel(
     const int nlong = s_nlong < kPrepLongBags ? s_nlong : kPrepLongBags;
     for (int j = 0; j < nlong; ++j) {
       const int lo = s_long[j];
-      for (int64_t i = s_off[lo] + threadIdx.x; i < s_off[lo + 1]; i += 256) emit(i, lo);
+      for (int64_t i = s_off[lo] + threadIdx.x; i < s_off[lo + 1]; i += kPrepThreads) emit(i, lo);
     }
   } else {
-    for (int64_t i = first + threadIdx.x; i < last; i += 256) {
+    for (int64_t i = first + threadIdx.x; i < last; i += kPrepThreads) {
       int lo = 0, hi = nb;  // find bag: s_off[lo] <= i < s_off[lo+1]
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -597,6 +600,8 @@ struct FlagScan {
 
 __device__ __forceinline__ void tile_flag_scan(const bool (&flag)[kSortItems], uint32_t *s_cnt,
                                                FlagScan &out, uint32_t *tile_total) {
+  constexpr int kWaves = kSortThreads / 64;
+  static_assert(kSortItems * kWaves == 64, "one count per (item, wave) pair, scanned by one wave");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -606,7 +611,7 @@ __device__ __forceinline__ void tile_flag_scan(const bool (&flag)[kSortItems], u
   for (int k = 0; k < kSortItems; ++k) {
     const uint64_t b = __ballot(flag[k]);
     within[k] = __popcll(b & le);
-    if (lane == 0) s_cnt[k * 4 + wave] = __popcll(b);
+    if (lane == 0) s_cnt[k * kWaves + wave] = __popcll(b);
   }
   __syncthreads();
   if (tid < 64) {  // 64 counts in (item, wave) order -> exclusive scan
@@ -621,7 +626,7 @@ __device__ __forceinline__ void tile_flag_scan(const bool (&flag)[kSortItems], u
   }
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < kSortItems; ++k) out.incl[k] = s_cnt[64 + k * 4 + wave] + within[k];
+  for (int k = 0; k < kSortItems; ++k) out.incl[k] = s_cnt[64 + k * kWaves + wave] + within[k];
   *tile_total = s_cnt[128];
 }
 
@@ -682,12 +687,12 @@ __device__ __forceinline__ uint32_t block_prefix_of_counts(const uint32_t *__res
 }
 
 // First occurrences (head_flag bytes, 0 or 1) in each kSortTile tile of
-// occurrences: 16 flags per thread (the flag array holds whole tiles).
+// occurrences: 4 flags per thread (the flag array holds whole tiles).
 __global__ __launch_bounds__(kSortThreads) void first_count_kernel(const uint8_t *__restrict__ head_flag,
                                                                   uint32_t *__restrict__ counts) {
-  static_assert(kSortTile == kSortThreads * 16, "one 16-byte vector of flags per thread");
-  const uint4 f = reinterpret_cast<const uint4 *>(head_flag)[blockIdx.x * kSortThreads + threadIdx.x];
-  uint32_t c = __popc(f.x) + __popc(f.y) + __popc(f.z) + __popc(f.w);
+  static_assert(kSortTile == kSortThreads * 4, "one 4-byte word of flags per thread");
+  const uint32_t f = reinterpret_cast<const uint32_t *>(head_flag)[blockIdx.x * kSortThreads + threadIdx.x];
+  uint32_t c = __popc(f);
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
   __shared__ uint32_t s_sum[kSortThreads / 64];
@@ -1477,12 +1482,12 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   const int pgrid = static_cast<int>(ceil_div(bags, bpb));
   float *aux = pooling == FLARE_POOL_MEAN ? w.aux : nullptr;
   if (id_dtype == FLARE_INT32)
-    prepare_csr_kernel<int32_t><<<pgrid, 256, 0, s>>>(
+    prepare_csr_kernel<int32_t><<<pgrid, kPrepThreads, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
         plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
         table_major, err);
   else
-    prepare_csr_kernel<int64_t><<<pgrid, 256, 0, s>>>(
+    prepare_csr_kernel<int64_t><<<pgrid, kPrepThreads, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
         plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
         table_major, err);

@@ -5,8 +5,11 @@
 
 namespace flare {
 
-constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
+// Scan-type passes over sorted keys and occurrences (head counts, runs, first
+// counts, ranks): 4096-position tiles of 1024 threads x 4 positions, so that
+// a call of a few thousand tiles keeps 16 waves of each CU busy.
+constexpr int kSortThreads = 1024;
+constexpr int kSortItems = 4;
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 occurrences per tile
 // Radix passes use larger tiles: 1024 threads x 8 keys (one tile per CU).
 constexpr int kOneThreads = 1024;
