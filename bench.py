@@ -733,6 +733,10 @@ def main() -> int:
                          "tables (the gradient transport dtype of the reference's BF16 and FP16 precision "
                          "policies, src/flare/jax/training/precision.py:62-69, cast before the gradient "
                          "leaves the JAX worker, train_worker.py:467-474), float32 for float32 tables")
+    ap.add_argument("--order", choices=["dedup-first", "forward-first"], default="forward-first",
+                    help="order of the step's first two phases on one stream: the dedup of the ids and then "
+                         "the pooled gather (the reference's order: unique ids before the lookup, "
+                         "src/flare/runtime/fluxway/workers/sparse_input.py:333-349), or the gather first")
     ap.add_argument("--overlap", action="store_true",
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
@@ -851,6 +855,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     order = []
+    fwd_start = [ev[0] for ev in events]  # the event before each step's forward
     for i in range(args.steps):
         k = (args.warmup + i) % len(plans)
         p = plans[k]
@@ -866,8 +871,15 @@ def main() -> int:
             p.forward()
             ev[1].record(stream)
             stream.wait_event(ev[3])
-        else:
+        elif args.order == "dedup-first":
+            ev[2] = ev[0]
+            p.dedup()
+            ev[3].record(stream)
+            fwd_start[i] = ev[3]
             p.forward()  # one launch: the pooled gather kernel
+            ev[1].record(stream)
+        else:
+            p.forward()
             ev[1].record(stream)
             ev[2] = ev[1]
             p.dedup()
@@ -875,7 +887,7 @@ def main() -> int:
         if overlap:
             ev[4].record(stream)
         else:
-            ev[4] = ev[3]
+            ev[4] = ev[1] if args.order == "dedup-first" else ev[3]
         _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
         p.apply(grad, grad_out=grad_out, optimizer=none_opt)
         ev[5].record(stream)
@@ -898,7 +910,7 @@ def main() -> int:
     sums_ms, fold_ms, applyk_ms, sums_gbs, applyk_gbs = [], [], [], [], []
     for i, ev in enumerate(events):
         b = batches[order[i]]
-        f = ev[0].elapsed_time(ev[1])
+        f = fwd_start[i].elapsed_time(ev[1])
         t = ev[0].elapsed_time(ev[5])
         a = ev[4].elapsed_time(ev[5])
         step_ms.append(t)
@@ -964,7 +976,9 @@ def main() -> int:
             "ids_per_step": w0.num_ids,
             "unique_per_step": uniques[0],
             "rotated_batches": len(plans),
-            "dedup": "concurrent with the forward" if overlap else "after the forward, same stream",
+            "dedup": "concurrent with the forward" if overlap else
+                     ("before the forward, same stream" if args.order == "dedup-first" else
+                      "after the forward, same stream"),
             "pooled_layout": "[T, B, D]" if args.layout == "table_major" else "[B, T, D]",
             "pooled_grad_dtype": grad_dtype,
         },

@@ -15,6 +15,8 @@ namespace flare {
 namespace {
 
 constexpr int kThreads = 256;
+// launch_pooled_short: shape not covered, use pooled_kernel
+constexpr int FLARE_NOT_HANDLED = -1;
 
 // ----------------------------------------------------------------------------
 // gather: raw row copy in units of CH bytes (bit-exact, like K1/K3).
@@ -300,6 +302,139 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   }
 }
 
+// Short CSR bags (at most kShortBagLength ids per bag on average, e.g. one id
+// per bag): one lane group of G lanes per kShortRows consecutive output rows.
+// Lane k of the group reads bag k's offsets and table range and resolves its
+// first id, so the group's kShortRows rows are gathered with all their loads
+// in flight; the remaining ids of a longer bag follow one at a time.  Each
+// pooled row is written as soon as it is done with 16-byte nontemporal
+// stores, kShortRows consecutive rows forming one contiguous range per group.
+// Accumulation as in pooled_kernel: fp32 from zero in occurrence order, the
+// mean divides by the number of valid ids (at least 1).
+constexpr int64_t kShortBagLength = 2;
+constexpr int kShortRows = 4;
+
+template <typename Tag, int VEC, int G, int L, typename IdT>
+__global__ __launch_bounds__(kThreads) void pooled_short_kernel(PooledArgs a) {
+  static_assert(G >= kShortRows, "one lane per bag of the group");
+  using E = typename Tag::elem;
+  using R = RawVec<Tag, VEC>;
+  constexpr int kGroups = kThreads / G;
+  const int lane = threadIdx.x % G;
+  const int64_t o0 = (static_cast<int64_t>(blockIdx.x) * kGroups + threadIdx.x / G) * kShortRows;
+  if (o0 >= a.bags) return;  // whole groups: the kernel has no barrier
+  const E *table = static_cast<const E *>(a.table);
+  E *out = static_cast<E *>(a.out);
+  const int D = a.dim;
+  const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
+  const bool mean = a.pooling == FLARE_POOL_MEAN;
+
+  // lane k < kShortRows: bag of output row o0 + k, its ids [lo, lo + len), its table range
+  int64_t lo = 0, len = 0, base = 0, rows = 0, first = -1;
+  float first_w = 1.0f;
+  if (lane < kShortRows && o0 + lane < a.bags) {
+    const int64_t o = o0 + lane;
+    int64_t t, bag;
+    if (a.table_major) {
+      t = o / a.batch;
+      bag = o;
+    } else {
+      const int64_t b = o / a.num_tables;
+      t = o - b * a.num_tables;
+      bag = t * a.batch + b;
+    }
+    int64_t hi;
+    lo = a.offsets[bag];
+    hi = a.offsets[bag + 1];
+    // offsets must start at 0, end at num_ids and never decrease
+    if (lo < 0 || hi > a.num_ids || hi < lo || (bag == 0 && lo != 0) || (bag + 1 == a.bags && hi != a.num_ids))
+      record_error(a.err, kErrIndexOutOfRange);
+    lo = lo < 0 ? 0 : (lo > a.num_ids ? a.num_ids : lo);
+    hi = hi < lo ? lo : (hi > a.num_ids ? a.num_ids : hi);  // decreasing offsets pool nothing
+    len = hi - lo;
+    base = a.row_base[t];
+    rows = a.row_base[t + 1] - base;
+    if (len > 0) {
+      first = resolve_row<true, IdT>(a, lo, base, base + rows);
+      if (weighted) first_w = a.weights[lo];
+    }
+  }
+  for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
+    R raw[kShortRows][L];
+    int64_t row_k[kShortRows];
+#pragma unroll
+    for (int k = 0; k < kShortRows; ++k) {
+      row_k[k] = __shfl(first, k, G);
+#pragma unroll
+      for (int q = 0; q < L; ++q) {
+        const int col = c0 + (q * G + lane) * VEC;
+        raw[k][q] = (row_k[k] >= 0 && col < D) ? load_raw<Tag, VEC>(table + row_k[k] * D + col) : R{};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kShortRows; ++k) {
+      const int64_t o = o0 + k;
+      if (o >= a.bags) break;
+      const int64_t blen = __shfl(len, k, G);
+      const int64_t blo = __shfl(lo, k, G);
+      const int64_t bbase = __shfl(base, k, G);
+      const int64_t brows = __shfl(rows, k, G);
+      const float bw = __shfl(first_w, k, G);
+      float acc[L][VEC];
+      int count = 0;
+#pragma unroll
+      for (int q = 0; q < L; ++q)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[q][v] = 0.0f;
+      if (row_k[k] >= 0) {
+        ++count;
+#pragma unroll
+        for (int q = 0; q < L; ++q) {
+          float x[VEC];
+          raw_to_f32<Tag, VEC>(raw[k][q], x);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            if (weighted) acc[q][v] += bw * x[v];
+            else acc[q][v] += x[v];
+          }
+        }
+      }
+      for (int64_t i = blo + 1; i < blo + blen; ++i) {  // ids after the first (longer bags)
+        const int64_t row = resolve_row<true, IdT>(a, i, bbase, bbase + brows);
+        if (row < 0) continue;
+        const float w = weighted ? a.weights[i] : 1.0f;
+        ++count;
+#pragma unroll
+        for (int q = 0; q < L; ++q) {
+          const int col = c0 + (q * G + lane) * VEC;
+          float x[VEC];
+          if (col < D) {
+            load_as_f32<Tag, VEC>(table + row * D + col, x);
+          } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) x[v] = 0.0f;
+          }
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            if (weighted) acc[q][v] += w * x[v];
+            else acc[q][v] += x[v];
+          }
+        }
+      }
+      const float div = static_cast<float>(count > 0 ? count : 1);
+#pragma unroll
+      for (int q = 0; q < L; ++q) {
+        if (mean) {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[q][v] = acc[q][v] / div;
+        }
+        const int col = c0 + (q * G + lane) * VEC;
+        if (col < D) store_from_f32_stream<Tag, VEC>(out + o * D + col, acc[q]);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------
@@ -343,6 +478,32 @@ int group_size(int vectors, int min_g) {
   return g;
 }
 
+template <typename Tag, int VEC, typename IdT>
+int launch_pooled_short(const PooledArgs &a, int vectors, hipStream_t s) {
+  // one 16-byte vector per lane and chunk: G lanes (at least kShortRows), L chunks per row
+  int G = kShortRows;
+  while (G < vectors && G < 64) G <<= 1;
+  const int L = static_cast<int>(ceil_div(vectors, G));
+  const int grid = grid_for(a.bags, static_cast<int64_t>(kThreads / G) * kShortRows);
+#define FLARE_SHORT(G_, L_) pooled_short_kernel<Tag, VEC, G_, L_, IdT><<<grid, kThreads, 0, s>>>(a)
+  if (L == 1) {
+    switch (G) {
+      case 4: FLARE_SHORT(4, 1); break;
+      case 8: FLARE_SHORT(8, 1); break;
+      case 16: FLARE_SHORT(16, 1); break;
+      case 32: FLARE_SHORT(32, 1); break;
+      default: FLARE_SHORT(64, 1); break;
+    }
+  } else if (L == 2) {
+    FLARE_SHORT(64, 2);
+  } else {
+    return FLARE_NOT_HANDLED;
+  }
+#undef FLARE_SHORT
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
 template <typename Tag, bool kCsr, typename IdT>
 int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   constexpr int kWide = 16 / sizeof(typename Tag::elem);
@@ -350,6 +511,12 @@ int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   const int64_t ids = kCsr ? a.num_ids : a.bags * a.max_elements;
   if (wide) {
     const int vectors = a.dim / kWide;  // 16-byte vectors per row
+    if constexpr (kCsr) {
+      if (ids <= kShortBagLength * a.bags) {
+        const int st = launch_pooled_short<Tag, kWide, IdT>(a, vectors, s);
+        if (st != FLARE_NOT_HANDLED) return st;
+      }
+    }
     if (vectors <= 64 && ids >= kLongBagLength * a.bags)
       return launch_pooled_g<Tag, kWide, 1, kCsr, IdT, true>(a, group_size(vectors, 4), s);
     if (vectors >= 8) return launch_pooled_g<Tag, kWide, 2, kCsr, IdT, false>(a, group_size(vectors / 2, 4), s);

@@ -359,15 +359,17 @@ def test_pooled_step_with_a_key_past_the_fold_chunk(gpu_device, no_device_errors
     no_device_errors()
 
 
-SHORT_DIMS = {"bfloat16": (64, 128, 256), "float16": (64, 128, 256), "float32": (32, 64, 128)}
+# 16-byte vectors per row: 8, 16, 32 (one per lane), 4 (the narrowest group) and 128 (two per lane)
+SHORT_DIMS = {"bfloat16": (64, 128, 256, 32, 1024), "float16": (64, 128, 256, 32, 1024),
+              "float32": (32, 64, 128, 16, 512)}
 
 
 @pytest.mark.parametrize("layout", ["sample_major", "table_major"])
 @pytest.mark.parametrize("pooling", ["sum", "mean", "weighted"])
 @pytest.mark.parametrize("storage", ["bfloat16", "float16", "float32"])
-@pytest.mark.parametrize("width", [0, 1, 2])
+@pytest.mark.parametrize("width", [0, 1, 2, 3, 4])
 def test_short_bag_forward_bit_exact(gpu_device, no_device_errors, layout, pooling, storage, width):
-    """Bags of 0-2 ids (at most 2 on average, a few of 3-5), rows of 128, 256 and 512 bytes,
+    """Bags of 0-2 ids (at most 2 on average, a few of 3-5), rows of 4 to 128 16-byte vectors,
     int32 and int64 ids, both pooled row layouts: the forward against the oracle."""
     from flare_amd.store import PooledTableShard, Uniform
 
@@ -396,6 +398,37 @@ def test_short_bag_forward_bit_exact(gpu_device, no_device_errors, layout, pooli
     assert tuple(pooled.shape) == shard.pooled_shape(batch)
     np.testing.assert_array_equal(_host(pooled), expected)
     no_device_errors()
+
+
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_short_bag_forward_skips_invalid_ids(gpu_device, no_device_errors, pooling):
+    """Short bags with some ids past their table: those ids pool nothing (nor count for the
+    mean) and set the error bit; every row equals the oracle's pooling of the valid ids."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    rng = np.random.default_rng(23)
+    table_rows, batch, dim = [50, 7, 300], 400, 128
+    lengths = rng.integers(0, 3, size=len(table_rows) * batch)
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    limit = np.asarray(table_rows)[bag_table]
+    ids = rng.integers(0, 1 << 20, size=int(offsets[-1])) % limit
+    bad = np.zeros(ids.size, bool)
+    bad[3::37] = True
+    ids = np.where(bad, limit + rng.integers(0, 5, size=ids.size), ids).astype(np.int64)
+    shard = PooledTableShard(table_rows, dim, value_dtype="bfloat16", initializer=Uniform(-1.0, 1.0), seed=2,
+                             layout="table_major")
+    pooled = shard.lookup_pooled(ids, offsets, batch, pooling=pooling)
+    shard.synchronize()
+    keep_len = np.add.reduceat(~bad, offsets[:-1]) * (lengths > 0)
+    keep_off = np.zeros(lengths.size + 1, np.int64)
+    keep_off[1:] = np.cumsum(keep_len)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    expected = O.gather_pooled_csr(_host(shard.table), ids[~bad], keep_off, row_base, batch, dim,
+                                   storage="bfloat16", pooling=pooling)
+    np.testing.assert_array_equal(_host(pooled), np.ascontiguousarray(expected.transpose(1, 0, 2)))
+    no_device_errors(1)
 
 
 @pytest.mark.parametrize("config", [2, 4])
