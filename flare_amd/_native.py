@@ -22,6 +22,7 @@ FLOAT32, FLOAT16, BFLOAT16, INT32, INT64, UINT32, UINT64 = range(7)
 POOL_SUM, POOL_MEAN, POOL_WEIGHTED = range(3)
 # flare_layout
 LAYOUT_SAMPLE_MAJOR, LAYOUT_TABLE_MAJOR = range(2)
+LAYOUT_ONE_ID_PER_BAG = 0x100  # flag for the dedup: every bag holds exactly one id
 # flare_optimizer_kind
 OPT_NONE, OPT_SGD, OPT_ADAM, OPT_ROWWISE_ADAGRAD = range(4)
 

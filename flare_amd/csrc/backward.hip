@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_csr_kernel(
     int bags_per_block, const int64_t *__restrict__ row_base, int32_t num_tables, int64_t batch,
     int64_t key_limit, int passes, int digit, uint32_t *__restrict__ keys, uint32_t *__restrict__ grad_row,
     float *__restrict__ aux, uint32_t *__restrict__ hist, uint32_t *__restrict__ reject, int per_bag,
-    int table_major, int *err) {
+    int table_major, int one_id, uint32_t *__restrict__ ident_flag, int *err) {
   __shared__ uint32_t s_hist[kMaxHistBins];
   __shared__ int64_t s_off[kPrepMaxBags + 1];
   for (int i = threadIdx.x; i < (passes << digit); i += kPrepThreads) s_hist[i] = 0;
@@ -336,10 +336,14 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_csr_kernel(
   }
   __syncthreads();
   for (int i = threadIdx.x; i < nb; i += kPrepThreads)
-    if (s_off[i + 1] < s_off[i]) {
+    if (s_off[i + 1] < s_off[i] || (one_id && s_off[i + 1] - s_off[i] != 1)) {
       record_error(err, kErrIndexOutOfRange);
       *reject = 1;
     }
+  // one id per bag in table-major order: occurrence i is pooled row i, which the
+  // update kernels use in place of a stored gradient row (workspace word 6)
+  const bool ident = one_id && table_major;
+  if (ident && blockIdx.x == 0 && threadIdx.x == 0) *ident_flag = 1;
   const int64_t first = s_off[0];
   const int64_t last = s_off[nb];
   const uint32_t sentinel = static_cast<uint32_t>(key_limit);
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_csr_kernel(
       record_error(err, kErrIndexOutOfRange);
     }
     keys[i] = k;
-    grad_row[i] = static_cast<uint32_t>(table_major ? bag : b * num_tables + t);
+    if (!ident) grad_row[i] = static_cast<uint32_t>(table_major ? bag : b * num_tables + t);
     if (aux) aux[i] = static_cast<float>(s_off[lo + 1] - s_off[lo]);
     add_histograms(s_hist, k, passes, digit);
   };
@@ -731,7 +735,7 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
     uint8_t *__restrict__ head_flag, uint2 *__restrict__ head_run,
     uint32_t *__restrict__ meta, const uint32_t *__restrict__ head_prefix, int fused_prefix,
     uint32_t *__restrict__ run_key,
-    const uint32_t *__restrict__ grad_row, int grad_sorted, const float *__restrict__ scale,
+    const uint32_t *__restrict__ grad_row, int grad_sorted, int grad_ident, const float *__restrict__ scale,
     uint32_t *__restrict__ sorted_grad_row, float *__restrict__ sorted_scale,
     uint32_t *__restrict__ run_grad_row, float *__restrict__ run_scale, const uint32_t *reject) {
   __shared__ uint32_t s_cnt[160];
@@ -792,8 +796,11 @@ __global__ __launch_bounds__(kSortThreads) void runs_kernel(
         head_run[o] = make_uint2(r, static_cast<uint32_t>(key[k]));
       }
       // per sorted position: the gradient row and scale of its occurrence
-      // (grad_sorted: the sort has already put the rows in sorted order)
-      if (sorted_grad_row) {
+      // (grad_sorted: the sort has already put the rows in sorted order;
+      // grad_ident: the occurrence is the row)
+      if (grad_ident) {
+        if (head[k]) run_grad_row[r] = o;
+      } else if (sorted_grad_row) {
         if (grad_sorted) {
           if (head[k]) run_grad_row[r] = sorted_grad_row[j];
         } else {
@@ -947,6 +954,7 @@ struct RunsOutputs {
   uint32_t *run_key;              // or null
   const uint32_t *grad_row;       // gathered into sorted order when non-null
   int grad_sorted;                // 1: the sort carried the rows into sorted order
+  int grad_ident;                 // 1: each occurrence is its own gradient row (not stored)
   const float *scale;             // gathered into sorted order when non-null
   int64_t *first_indices;         // or null
   void *unique_out;               // or null
@@ -966,7 +974,7 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
   if (!fused) scan_counts_kernel<<<1, 1024, 0, s>>>(head_prefix, w.tiles);
   runs_kernel<K><<<w.tiles, kSortThreads, 0, s>>>(
       sk, sv, n, sentinel, use_sentinel, w.run_start, w.unit_first_run, w.head_flag, w.head_run,
-      w.meta, head_prefix, fused, o.run_key, o.grad_row, o.grad_sorted, o.scale,
+      w.meta, head_prefix, fused, o.run_key, o.grad_row, o.grad_sorted, o.grad_ident, o.scale,
       o.grad_row ? w.sorted_grad_row : nullptr, o.scale ? w.sorted_scale : nullptr,
       w.run_grad_row, w.run_scale, w.meta + 3);
   first_count_kernel<<<w.tiles, kSortThreads, 0, s>>>(w.head_flag, first_prefix);
@@ -984,13 +992,14 @@ int runs_and_rank(const Workspace &w, const K *sk, const uint32_t *sv, uint32_t 
 int dedup_rows(const Workspace &w, const RadixPlan &plan, uint32_t sentinel, int *err, hipStream_t s,
                int *sorted, int64_t *first_indices, void *unique_out, int unique_source,
                const void *values, int value_bytes, int64_t *unique_count,
-               const float *scale_src) {
-  const bool carry = carries_grad_rows(w, plan, 4);
+               const float *scale_src, bool grad_ident = false) {
+  // grad_ident: the occurrence is its own gradient row, nothing to carry or gather
+  const bool carry = !grad_ident && carries_grad_rows(w, plan, 4);
   FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, sorted, carry));
   const uint32_t n = static_cast<uint32_t>(w.n);
   const uint32_t *sk = static_cast<const uint32_t *>(w.keys[*sorted]);
-  RunsOutputs o{w.run_key, w.grad_row, carry ? 1 : 0, scale_src, first_indices, unique_out, unique_source,
-                values, value_bytes, unique_count};
+  RunsOutputs o{w.run_key, w.grad_row, carry ? 1 : 0, grad_ident ? 1 : 0, scale_src, first_indices, unique_out,
+                unique_source, values, value_bytes, unique_count};
   return runs_and_rank<uint32_t>(w, sk, w.vals[*sorted], n, sentinel, 1, o, s);
 }
 
@@ -1232,7 +1241,7 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
     FLARE_TRY_HIP(hipGetLastError());
     int sorted = 0;
     FLARE_TRY(run_sort<uint32_t>(w, plan, err, s, &sorted));
-    RunsOutputs o{w.run_key, nullptr, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+    RunsOutputs o{w.run_key, nullptr, 0, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                   values, value_bytes, unique_count};
     FLARE_TRY(runs_and_rank<uint32_t>(w, static_cast<const uint32_t *>(w.keys[sorted]), w.vals[sorted],
                                       static_cast<uint32_t>(n), 0u, 0, o, s));
@@ -1252,7 +1261,7 @@ int unique_typed(const SrcT *values, int64_t n, int64_t key_bound, void *unique_
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   FLARE_TRY(run_sort<uint64_t>(w, plan, err, s, &sorted));
-  RunsOutputs o{nullptr, nullptr, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
+  RunsOutputs o{nullptr, nullptr, 0, 0, nullptr, first_indices_out, unique_out, kUniqueFromValues,
                 values, value_bytes, unique_count};
   FLARE_TRY(runs_and_rank<uint64_t>(w, static_cast<const uint64_t *>(w.keys[sorted]), w.vals[sorted],
                                     static_cast<uint32_t>(n), 0ull, 0, o, s));
@@ -1444,7 +1453,8 @@ int check_pooled_args(int64_t rows, int32_t dim, int32_t num_tables, int64_t bat
 }
 
 int check_layout(int32_t layout) {
-  if (layout != FLARE_LAYOUT_SAMPLE_MAJOR && layout != FLARE_LAYOUT_TABLE_MAJOR)
+  const int32_t base = layout & ~FLARE_LAYOUT_ONE_ID_PER_BAG;
+  if (base != FLARE_LAYOUT_SAMPLE_MAJOR && base != FLARE_LAYOUT_TABLE_MAJOR)
     return fail(FLARE_ERR_ARGUMENT, "unknown pooled row layout %d", layout);
   return FLARE_OK;
 }
@@ -1461,7 +1471,8 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
     return fail(FLARE_ERR_DTYPE, "CSR ids must be int32 or int64, got dtype code %d", id_dtype);
   FLARE_TRY(check_pooled_args(rows, dim, num_tables, batch, n, pooling, nullptr, false));
   FLARE_TRY(check_layout(layout));
-  const int table_major = layout == FLARE_LAYOUT_TABLE_MAJOR ? 1 : 0;
+  const int table_major = (layout & ~FLARE_LAYOUT_ONE_ID_PER_BAG) == FLARE_LAYOUT_TABLE_MAJOR ? 1 : 0;
+  const int one_id = (layout & FLARE_LAYOUT_ONE_ID_PER_BAG) ? 1 : 0;
   hipStream_t s = as_stream(stream);
   const int64_t bags = batch * num_tables;
   if (n == 0 || bags == 0) {
@@ -1485,16 +1496,17 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
     prepare_csr_kernel<int32_t><<<pgrid, kPrepThreads, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
         plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
-        table_major, err);
+        table_major, one_id, w.meta + 6, err);
   else
     prepare_csr_kernel<int64_t><<<pgrid, kPrepThreads, 0, s>>>(
         static_cast<const int64_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
         plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
-        table_major, err);
+        table_major, one_id, w.meta + 6, err);
   FLARE_TRY_HIP(hipGetLastError());
   int sorted = 0;
   return dedup_rows(w, plan, sentinel, err, s, &sorted, first_indices_out, unique_out,
-                    unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count, aux);
+                    unique_out ? kUniqueFromSorted : kUniqueNone, nullptr, 0, unique_count, aux,
+                    one_id && table_major);
 }
 
 extern "C" int flare_pooled_apply(void *table, int32_t value_dtype, int64_t rows, int32_t dim,

@@ -37,7 +37,8 @@ struct Workspace {
   // zero-initialized region (first)
   uint32_t *hist;         // [kHistCopies][kMaxPasses][kMaxRadix] digit histograms
   uint32_t *tickets;      // [16] tile tickets (8 sort passes, runs, rank)
-  uint32_t *meta;         // [8]: nvalid, unique count, hot-key count, rejected batch, non-finite gradient
+  uint32_t *meta;         // [8]: nvalid, unique count, hot-key count, rejected batch, non-finite gradient,
+                          //      (unused), occurrences are their own gradient rows
   uint32_t *sort_status;  // [passes][sort_tiles][2^digit bits] (last in the zeroed region)
   uint32_t *scan_status;  // [2][tiles]
   uint8_t *head_flag;     // [tiles * kSortTile] 1 at o: occurrence o is its key's first (else 0)

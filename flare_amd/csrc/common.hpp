@@ -265,6 +265,10 @@ __device__ __forceinline__ uint32_t peek(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// kWindow predecessors are read per round trip: when every tile of a pass is
+// resident at once (one per CU), the inclusive prefixes spread back to front
+// about 2 * kWindow tiles per round trip.
+template <int kWindow = 4>
 __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_t tile,
                                                        uint32_t stride, uint32_t idx,
                                                        uint32_t value, int *err) {
@@ -274,18 +278,18 @@ __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_
     return 0;
   }
   publish(mine, kFlagAggregate | value);
-  // Walk back over predecessors, four status words per round trip.
+  // Walk back over predecessors, kWindow status words per round trip.
   uint32_t prefix = 0;
   int64_t t = static_cast<int64_t>(tile) - 1;
   uint32_t spins = 0;
   bool done = false;
   while (t >= 0 && !done) {
-    uint32_t seen[4];
+    uint32_t seen[kWindow];
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+    for (int w = 0; w < kWindow; ++w)
       seen[w] = (t - w >= 0) ? peek(status + static_cast<size_t>(t - w) * stride + idx) : kFlagPrefix;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kWindow; ++w) {
       if (done) break;
       uint32_t st = seen[w];
       while ((st & ~kCountMask) == 0) {  // predecessor has not published yet
@@ -300,7 +304,7 @@ __device__ __forceinline__ uint32_t lookback_exclusive(uint32_t *status, uint32_
       prefix += st & kCountMask;
       if ((st & ~kCountMask) == kFlagPrefix) done = true;
     }
-    t -= 4;
+    t -= kWindow;
   }
   publish(mine, kFlagPrefix | ((prefix + value) & kCountMask));
   return prefix;

@@ -15,6 +15,10 @@ namespace flare {
 // ----------------------------------------------------------------------------
 // update: deterministic segment reduction + optimizer
 // ----------------------------------------------------------------------------
+// Workspace word (UpdateArgs::meta) set by the CSR dedup when each occurrence
+// is its own gradient row (one id per bag, table-major rows): no gradient row
+// is stored or sorted, the sorted position's occurrence is the row.
+constexpr int kMetaGradIdent = 6;
 enum ApplyMode : int { kModeRows = 0, kModeUnique = 1, kModeSgd = 2, kModeAdam = 3, kModeAdagrad = 4 };
 enum GradRowMode : int { kGradRowOcc = 0, kGradRowDiv = 1, kGradRowArray = 2 };
 enum ScaleMode : int { kScaleNone = 0, kScaleMul = 1, kScaleDiv = 2 };
@@ -293,6 +297,7 @@ __device__ __forceinline__ float scaled(const UpdateArgs &a, float x, float sc) 
 template <typename Tag, int VEC, int G, int NC, int MODE, int kGrad>
 __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
   if (a.reject && *a.reject) return;
+  const bool ident = a.meta[kMetaGradIdent] != 0;
   constexpr int kGroups = 256 / G;
   constexpr int kPPL = kReduceUnit / G;  // sorted positions per lane in the prefetch
   constexpr bool kDirect = MODE == kModeRows || MODE == kModeUnique;
@@ -355,7 +360,8 @@ __global__ __launch_bounds__(256) void sums_kernel(UpdateArgs a) {
       lng = ps < 0 || cross_right || static_cast<uint32_t>(pe - ps) > kShortRun;
       if (lng) {
         const uint32_t j = j0 + p;
-        s_grow[group][p] = checked_grad_row(a, a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, occ[q]));
+        s_grow[group][p] = checked_grad_row(a, ident ? occ[q] : (a.sorted_grad_row ? a.sorted_grad_row[j]
+                                                                                   : grad_row_of(a, occ[q])));
         s_scale[group][p] = (a.scale_mode == kScaleNone) ? 1.0f
                             : (a.sorted_scale ? a.sorted_scale[j] : a.scale[occ[q]]);
         if constexpr (MODE == kModeRows) s_dest[group][p] = keyv[q];
@@ -527,7 +533,8 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
         if (a.scale_mode != kScaleNone) my_sc = a.run_scale[r];
       } else if (static_cast<uint32_t>(lane) < len) {
         const uint32_t j = seg_start + lane;
-        const bool need_occ = !a.sorted_grad_row || (a.scale_mode != kScaleNone && !a.sorted_scale);
+        const bool ident = a.meta[kMetaGradIdent] != 0;
+        const bool need_occ = ident || !a.sorted_grad_row || (a.scale_mode != kScaleNone && !a.sorted_scale);
         uint32_t o = 0;
         if (need_occ) {
           o = a.sv[j];
@@ -536,7 +543,7 @@ __global__ __launch_bounds__(256) void apply_kernel(UpdateArgs a) {
             o = 0;
           }
         }
-        my_gr = checked_grad_row(a, a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o));
+        my_gr = checked_grad_row(a, ident ? o : (a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o)));
         if (a.scale_mode != kScaleNone) my_sc = a.sorted_scale ? a.sorted_scale[j] : a.scale[o];
       }
       for (uint32_t k = 0; k < len; k += 4) {
@@ -713,6 +720,7 @@ __global__ __launch_bounds__(256) void piece_sums_kernel(UpdateArgs a) {
   const uint32_t j1 = active ? min(j0 + kReduceUnit, nvalid) : j0;
   const int cnt = static_cast<int>(j1 - j0);
   const int D = a.dim;
+  const bool ident = a.meta[kMetaGradIdent] != 0;
 
   uint32_t grow[kPPL];
   float scl[kPPL];
@@ -726,7 +734,7 @@ __global__ __launch_bounds__(256) void piece_sums_kernel(UpdateArgs a) {
     if (p < cnt) {
       const uint32_t j = j0 + p;
       head = (j == 0) || (a.sk[j] != a.sk[j - 1]);
-      const bool need_occ = !a.sorted_grad_row || (a.scale_mode != kScaleNone && !a.sorted_scale);
+      const bool need_occ = ident || !a.sorted_grad_row || (a.scale_mode != kScaleNone && !a.sorted_scale);
       uint32_t o = 0;
       if (need_occ) {
         o = a.sv[j];
@@ -735,7 +743,7 @@ __global__ __launch_bounds__(256) void piece_sums_kernel(UpdateArgs a) {
           o = 0;
         }
       }
-      grow[q] = checked_grad_row(a, a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o));
+      grow[q] = checked_grad_row(a, ident ? o : (a.sorted_grad_row ? a.sorted_grad_row[j] : grad_row_of(a, o)));
       if (a.scale_mode != kScaleNone) scl[q] = a.sorted_scale ? a.sorted_scale[j] : a.scale[o];
     }
     const uint64_t bal = __ballot(head);

@@ -940,6 +940,15 @@ class PooledStepPlan:
         self._id_code = _native.INT32 if self.ids.dtype == torch.int32 else _native.INT64
         self._stream = int(shard.stream.cuda_stream)
         self._dedup_stream: torch.cuda.Stream | None = None
+        # one id per bag (offsets 0, 1, 2, ...) in table-major order: the dedup is told, so that
+        # it keeps no gradient row per occurrence (it checks the claim on the device)
+        self._dedup_layout = shard._layout_code
+        bags = self.batch * shard.num_tables
+        if shard.layout == "table_major" and self.n == bags and bags > 0:
+            with torch.cuda.stream(shard.stream):
+                steps = torch.arange(bags + 1, dtype=self.offsets.dtype, device=dev)
+                if bool(torch.equal(self.offsets, steps)):
+                    self._dedup_layout |= _native.LAYOUT_ONE_ID_PER_BAG
         torch.cuda.current_stream(dev).wait_stream(shard.stream)
 
     def step(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
@@ -999,7 +1008,7 @@ class PooledStepPlan:
         _native.call(
             "flare_pooled_dedup", self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
             s.num_tables, self.batch, s.row_base.data_ptr(), s.total_rows, s.dim,
-            _POOLING[self.pooling], s._layout_code, self.unique.data_ptr(), self.first_indices.data_ptr(),
+            _POOLING[self.pooling], self._dedup_layout, self.unique.data_ptr(), self.first_indices.data_ptr(),
             self.unique_count.data_ptr(), self.workspace.data_ptr(), self.workspace_bytes, stream,
         )
 

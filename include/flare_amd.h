@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define FLARE_ABI_VERSION 2
+#define FLARE_ABI_VERSION 3
 
 /* Status codes; the Python layer maps them to the reference's exception
  * classes (src/flare/kernels/backends/gpu_cupy.py:351-354,398-401,479-483). */
@@ -59,7 +59,15 @@ typedef enum flare_pooling {
  * other: [T, B, D], row t*B + b, the bag order of the CSR batch itself. */
 typedef enum flare_layout {
   FLARE_LAYOUT_SAMPLE_MAJOR = 0,
-  FLARE_LAYOUT_TABLE_MAJOR = 1
+  FLARE_LAYOUT_TABLE_MAJOR = 1,
+  /* Flag for flare_pooled_dedup / flare_pooled_backward, OR'ed into
+   * FLARE_LAYOUT_TABLE_MAJOR: the caller states that every bag holds exactly
+   * one id (offsets[k] == k).  Occurrence i is then pooled row i, so the
+   * dedup neither stores nor sorts a gradient row per occurrence.  The dedup
+   * checks the statement: any bag of another length sets error bit 1 and
+   * rejects the batch (no runs, the update does nothing).  Ignored with
+   * SAMPLE_MAJOR; the pooled gather takes the plain layout values only. */
+  FLARE_LAYOUT_ONE_ID_PER_BAG = 0x100
 } flare_layout;
 
 typedef enum flare_optimizer_kind {

@@ -460,3 +460,102 @@ def test_table_major_step_matches_sample_major(gpu_device, no_device_errors, con
     for x, y in zip(a[1:], b[1:]):
         np.testing.assert_array_equal(x, y)
     no_device_errors()
+
+
+@pytest.mark.parametrize("pooling,optimizer", [("sum", "rowwise_adagrad"), ("mean", "adam"), ("weighted", "sgd"),
+                                               ("sum", "none"), ("weighted", "none")])
+def test_one_id_per_bag_plan_matches_oracle(gpu_device, no_device_errors, pooling, optimizer):
+    """Table-major plan over bags of exactly one id: the dedup keeps no gradient row per
+    occurrence (each occurrence is its own pooled row); step against the oracle."""
+    from flare_amd import _native
+    from flare_amd.store import Adam, PooledTableShard, RowWiseAdagrad, Sgd, Uniform
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    w = make_workload(2, batch=1800, row_scale=0.0005)
+    assert np.array_equal(w.offsets, np.arange(w.offsets.size))
+    weights = np.random.default_rng(4).uniform(0, 1, w.num_ids).astype(np.float32) if pooling == "weighted" else None
+    opt = {"rowwise_adagrad": RowWiseAdagrad(lr=0.01, eps=1e-8), "adam": Adam(lr=0.01), "sgd": Sgd(lr=0.01),
+           "none": RowWiseAdagrad()}[optimizer]
+    shard = PooledTableShard(w.table_rows, w.dim, value_dtype=w.value_dtype, optimizer=opt,
+                             initializer=Uniform(-0.01, 0.01), seed=9, layout="table_major")
+    table0 = _host(shard.table.clone())
+    grad = pooled_grad_host(w)  # [B, T, D]
+    plan = shard.plan_step(w.ids, w.offsets, w.batch, pooling=pooling, per_sample_weights=weights)
+    assert plan._dedup_layout & _native.LAYOUT_ONE_ID_PER_BAG
+    g = torch.from_numpy(np.ascontiguousarray(grad.transpose(1, 0, 2))).to(gpu_device)
+    grad_out = none_opt = None
+    if optimizer == "none":
+        grad_out = torch.empty((w.num_ids, w.dim), dtype=torch.float32, device=gpu_device)
+        none_opt = _native.FlareOptimizer()
+        none_opt.kind = _native.OPT_NONE
+    pooled = plan.forward()
+    plan.dedup()
+    plan.apply(g, grad_out=grad_out, optimizer=none_opt)
+    shard.synchronize()
+    u = int(plan.unique_count.item())
+    if optimizer == "none":
+        eu, ei, ef, eg = O.pooled_grad_sums(w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad,
+                                            pooling=pooling, weights=weights)
+        np.testing.assert_array_equal(plan.unique[:u].cpu().numpy(), eu)
+        np.testing.assert_array_equal(plan.inverse[:w.num_ids].cpu().numpy(), ei)
+        np.testing.assert_array_equal(plan.first_indices[:u].cpu().numpy(), ef)
+        np.testing.assert_array_equal(grad_out[:u].cpu().numpy(), eg)
+        np.testing.assert_array_equal(_host(shard.table), table0)
+    else:
+        state = {}
+        if optimizer == "rowwise_adagrad":
+            state = {"acc": np.zeros(w.total_rows, np.float32)}
+        elif optimizer == "adam":
+            state = {"m": np.zeros((w.total_rows, w.dim), np.float32),
+                     "v": np.zeros((w.total_rows, w.dim), np.float32), "step": np.zeros(w.total_rows, np.int32)}
+        e_pooled, e_table, e_state, e_unique, e_inverse, e_first = O.pooled_step(
+            table0, state, w.ids, w.offsets, w.row_base(), w.batch, w.dim, grad, storage=w.value_dtype,
+            pooling=pooling, weights=weights, optimizer=optimizer)
+        np.testing.assert_array_equal(_host(pooled), np.ascontiguousarray(e_pooled.transpose(1, 0, 2)))
+        np.testing.assert_array_equal(plan.unique[:u].cpu().numpy(), e_unique)
+        np.testing.assert_array_equal(plan.inverse[:w.num_ids].cpu().numpy(), e_inverse)
+        np.testing.assert_array_equal(plan.first_indices[:u].cpu().numpy(), e_first)
+        ulps = O.storage_ulp_distance(_host(shard.table), e_table, w.value_dtype)
+        assert ulps.max() <= 1, f"max ulp {ulps.max()}"
+        if optimizer == "rowwise_adagrad":
+            np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["acc"], rtol=1e-5, atol=0)
+        elif optimizer == "adam":
+            np.testing.assert_allclose(shard.state.state0.cpu().numpy(), e_state["m"], rtol=1e-5, atol=1e-12)
+            np.testing.assert_array_equal(shard.state.step.cpu().numpy(), e_state["step"])
+    no_device_errors()
+
+
+def test_one_id_per_bag_claim_is_checked(gpu_device, no_device_errors):
+    """The one-id-per-bag flag with a bag of two ids: error bit 1, no runs, no update."""
+    import ctypes
+
+    from flare_amd import _native
+    from flare_amd.store import PooledTableShard, RowWiseAdagrad, Uniform
+
+    shard = PooledTableShard([20, 20], 8, value_dtype="float32", optimizer=RowWiseAdagrad(lr=0.5),
+                             initializer=Uniform(-1.0, 1.0), seed=1, layout="table_major")
+    table0 = shard.table.clone()
+    batch = 3
+    offsets = torch.tensor([0, 1, 3, 4, 5, 6, 7], dtype=torch.int64, device=gpu_device)  # bag 1 holds 2 ids
+    ids = torch.tensor([1, 2, 3, 4, 5, 6, 7], dtype=torch.int64, device=gpu_device)
+    n = int(ids.numel())
+    lib = _native.library()
+    ws_bytes = lib.flare_pooled_backward_workspace_bytes(n, shard.total_rows, shard.dim)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu_device)
+    count = torch.full((1,), -1, dtype=torch.int64, device=gpu_device)
+    grad = torch.ones((2, batch, 8), dtype=torch.float32, device=gpu_device)
+    stream = int(torch.cuda.current_stream(gpu_device).cuda_stream)
+    torch.cuda.synchronize()
+    layout = _native.LAYOUT_TABLE_MAJOR | _native.LAYOUT_ONE_ID_PER_BAG
+    _native.call("flare_pooled_dedup", ids.data_ptr(), _native.INT64, n, offsets.data_ptr(), 2, batch,
+                 shard.row_base.data_ptr(), shard.total_rows, 8, 0, layout, None, None, count.data_ptr(),
+                 ws.data_ptr(), ws_bytes, stream)
+    opt = shard.state.native_optimizer
+    s0, s1, st = shard.state.pointers()
+    _native.call("flare_pooled_apply", shard.table.data_ptr(), _native.FLOAT32, shard.total_rows, 8, s0, s1, st,
+                 ctypes.byref(opt), n, 2, batch, 0, None, grad.data_ptr(), 1, None, None, ws.data_ptr(), ws_bytes,
+                 stream)
+    torch.cuda.synchronize()
+    assert int(count.item()) == 0
+    assert torch.equal(shard.table, table0)
+    no_device_errors(1)
