@@ -64,6 +64,7 @@ struct PooledArgs {
   int32_t pad_index;
   int32_t pooling;
   int32_t table_major;  // CSR: output row o is bag o ([T, B, D]) instead of b*T + t
+  int32_t one_id;       // CSR, table-major: every bag holds one id (offsets[k] == k, checked)
   const float *weights;
   void *out;
   int64_t bags;
@@ -104,10 +105,8 @@ constexpr int bags_per_group(int g) {
 }
 
 // Resolve one id to a table row (or -1 for a pad / out-of-range slot).
-template <bool kCsr, typename IdT>
-__device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, int64_t row_lo,
-                                               int64_t row_hi) {
-  const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]);
+template <bool kCsr>
+__device__ __forceinline__ int64_t resolve_id(const PooledArgs &a, int64_t id, int64_t row_lo, int64_t row_hi) {
   if constexpr (kCsr) {
     // inside the table's own range and inside the whole table (a row_base
     // whose entries run past table_rows must not read beyond it)
@@ -120,6 +119,12 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
     record_error(a.err, kErrIndexOutOfRange);
     return -1;
   }
+}
+
+template <bool kCsr, typename IdT>
+__device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, int64_t row_lo,
+                                               int64_t row_hi) {
+  return resolve_id<kCsr>(a, static_cast<int64_t>(static_cast<const IdT *>(a.ids)[i]), row_lo, row_hi);
 }
 
 // A block pools kBagsPerBlock consecutive OUTPUT rows (CSR: output row
@@ -306,7 +311,10 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
 // per bag): one lane group of G lanes per kShortRows consecutive output rows.
 // Lane k of the group reads bag k's offsets and table range and resolves its
 // first id, so the group's kShortRows rows are gathered with all their loads
-// in flight; the remaining ids of a longer bag follow one at a time.  Each
+// in flight; the remaining ids of a longer bag follow one at a time.  The
+// first id is loaded together with the offsets, from occurrence `bag` (where
+// it is when every bag before this one holds one id), and used when the
+// offsets confirm it: one dependent load fewer before the row.  Each
 // pooled row is written as soon as it is done with 16-byte nontemporal
 // stores, kShortRows consecutive rows forming one contiguous range per group.
 // Accumulation as in pooled_kernel: fp32 from zero in occurrence order, the
@@ -343,6 +351,11 @@ __global__ __launch_bounds__(kThreads) void pooled_short_kernel(PooledArgs a) {
       t = o - b * a.num_tables;
       bag = t * a.batch + b;
     }
+    // speculative first id and weight of the bag, read with its offsets
+    const int64_t guess = bag < a.num_ids ? bag : 0;
+    const bool can_guess = bag < a.num_ids;
+    const int64_t guess_id = can_guess ? static_cast<int64_t>(static_cast<const IdT *>(a.ids)[guess]) : 0;
+    const float guess_w = (can_guess && weighted) ? a.weights[guess] : 1.0f;
     int64_t hi;
     lo = a.offsets[bag];
     hi = a.offsets[bag + 1];
@@ -355,8 +368,13 @@ __global__ __launch_bounds__(kThreads) void pooled_short_kernel(PooledArgs a) {
     base = a.row_base[t];
     rows = a.row_base[t + 1] - base;
     if (len > 0) {
-      first = resolve_row<true, IdT>(a, lo, base, base + rows);
-      if (weighted) first_w = a.weights[lo];
+      if (can_guess && lo == bag) {
+        first = resolve_id<true>(a, guess_id, base, base + rows);
+        first_w = guess_w;
+      } else {
+        first = resolve_row<true, IdT>(a, lo, base, base + rows);
+        if (weighted) first_w = a.weights[lo];
+      }
     }
   }
   for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
@@ -435,6 +453,80 @@ __global__ __launch_bounds__(kThreads) void pooled_short_kernel(PooledArgs a) {
   }
 }
 
+// One id per bag in table-major order (FLARE_LAYOUT_ONE_ID_PER_BAG, checked):
+// output row o is bag o and occurrence o.  One lane group of G lanes per
+// kShortRows consecutive rows; lane k < kShortRows reads the id, weight and
+// both offsets of row o0 + k and its table's range, none of these loads
+// waiting on another, and the group then loads its rows together.  A bag
+// whose offsets are not (o, o + 1) sets error bit 1 and gets a zero row.  The
+// pooled row of one id is 0 + x (sum), (0 + x) / 1 (mean) or 0 + w * x
+// (weighted) in fp32, rounded to nearest even: the same bits pooled_short_kernel
+// writes for such a bag.
+template <typename Tag, int VEC, int G, int L, typename IdT>
+__global__ __launch_bounds__(kThreads) void pooled_one_kernel(PooledArgs a) {
+  static_assert(G >= kShortRows, "one lane per bag of the group");
+  using E = typename Tag::elem;
+  using R = RawVec<Tag, VEC>;
+  constexpr int kGroups = kThreads / G;
+  const int lane = threadIdx.x % G;
+  const int64_t o0 = (static_cast<int64_t>(blockIdx.x) * kGroups + threadIdx.x / G) * kShortRows;
+  if (o0 >= a.bags) return;  // whole groups: the kernel has no barrier
+  const E *table = static_cast<const E *>(a.table);
+  E *out = static_cast<E *>(a.out);
+  const int D = a.dim;
+  const bool weighted = a.pooling == FLARE_POOL_WEIGHTED;
+  const bool mean = a.pooling == FLARE_POOL_MEAN;
+  int64_t row = -1;
+  float w = 1.0f;
+  if (lane < kShortRows && o0 + lane < a.bags) {
+    const int64_t o = o0 + lane;  // < bags == num_ids (checked by the host)
+    const int64_t t = o / a.batch;
+    const int64_t id = static_cast<int64_t>(static_cast<const IdT *>(a.ids)[o]);
+    const float wo = weighted ? a.weights[o] : 1.0f;
+    const int64_t lo = a.offsets[o], hi = a.offsets[o + 1];
+    const int64_t base = a.row_base[t];
+    const int64_t rows = a.row_base[t + 1] - base;
+    if (lo == o && hi == o + 1) {
+      row = resolve_id<true>(a, id, base, base + rows);
+      w = wo;
+    } else {
+      record_error(a.err, kErrIndexOutOfRange);
+    }
+  }
+  for (int c0 = 0; c0 < D; c0 += G * VEC * L) {
+    R raw[kShortRows][L];
+    int64_t row_k[kShortRows];
+#pragma unroll
+    for (int k = 0; k < kShortRows; ++k) {
+      row_k[k] = __shfl(row, k, G);
+#pragma unroll
+      for (int q = 0; q < L; ++q) {
+        const int col = c0 + (q * G + lane) * VEC;
+        raw[k][q] = (row_k[k] >= 0 && col < D) ? load_raw<Tag, VEC>(table + row_k[k] * D + col) : R{};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kShortRows; ++k) {
+      const int64_t o = o0 + k;
+      if (o >= a.bags) break;
+      const float bw = __shfl(w, k, G);
+#pragma unroll
+      for (int q = 0; q < L; ++q) {
+        float x[VEC], acc[VEC];
+        raw_to_f32<Tag, VEC>(raw[k][q], x);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          acc[v] = 0.0f;
+          if (row_k[k] >= 0) acc[v] += weighted ? bw * x[v] : x[v];
+          if (mean) acc[v] = acc[v] / 1.0f;
+        }
+        const int col = c0 + (q * G + lane) * VEC;
+        if (col < D) store_from_f32_stream<Tag, VEC>(out + o * D + col, acc);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------
@@ -504,6 +596,31 @@ int launch_pooled_short(const PooledArgs &a, int vectors, hipStream_t s) {
   return FLARE_OK;
 }
 
+template <typename Tag, int VEC, typename IdT>
+int launch_pooled_one(const PooledArgs &a, int vectors, hipStream_t s) {
+  int G = kShortRows;
+  while (G < vectors && G < 64) G <<= 1;
+  const int L = static_cast<int>(ceil_div(vectors, G));
+  const int grid = grid_for(a.bags, static_cast<int64_t>(kThreads / G) * kShortRows);
+#define FLARE_ONE(G_, L_) pooled_one_kernel<Tag, VEC, G_, L_, IdT><<<grid, kThreads, 0, s>>>(a)
+  if (L == 1) {
+    switch (G) {
+      case 4: FLARE_ONE(4, 1); break;
+      case 8: FLARE_ONE(8, 1); break;
+      case 16: FLARE_ONE(16, 1); break;
+      case 32: FLARE_ONE(32, 1); break;
+      default: FLARE_ONE(64, 1); break;
+    }
+  } else if (L == 2) {
+    FLARE_ONE(64, 2);
+  } else {
+    return FLARE_NOT_HANDLED;
+  }
+#undef FLARE_ONE
+  FLARE_TRY_HIP(hipGetLastError());
+  return FLARE_OK;
+}
+
 template <typename Tag, bool kCsr, typename IdT>
 int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   constexpr int kWide = 16 / sizeof(typename Tag::elem);
@@ -512,6 +629,10 @@ int launch_pooled_tag(PooledArgs a, hipStream_t s) {
   if (wide) {
     const int vectors = a.dim / kWide;  // 16-byte vectors per row
     if constexpr (kCsr) {
+      if (a.one_id) {
+        const int st = launch_pooled_one<Tag, kWide, IdT>(a, vectors, s);
+        if (st != FLARE_NOT_HANDLED) return st;
+      }
       if (ids <= kShortBagLength * a.bags) {
         const int st = launch_pooled_short<Tag, kWide, IdT>(a, vectors, s);
         if (st != FLARE_NOT_HANDLED) return st;
@@ -625,15 +746,21 @@ extern "C" int flare_gather_pooled_csr(const void *table, int32_t value_dtype, i
   if (num_tables <= 0 || batch < 0 || dim <= 0 || table_rows < 0 || n < 0)
     return fail(FLARE_ERR_SHAPE, "invalid CSR pooled gather sizes");
   FLARE_TRY(check_pooling(pooling, weights));
+  const bool one_id = (layout & FLARE_LAYOUT_ONE_ID_PER_BAG) != 0;
+  layout &= ~FLARE_LAYOUT_ONE_ID_PER_BAG;
   if (layout != FLARE_LAYOUT_SAMPLE_MAJOR && layout != FLARE_LAYOUT_TABLE_MAJOR)
     return fail(FLARE_ERR_ARGUMENT, "unknown pooled row layout %d", layout);
   const int64_t bags = batch * num_tables;
+  if (one_id && layout == FLARE_LAYOUT_TABLE_MAJOR && n != bags)
+    return fail(FLARE_ERR_SHAPE, "one id per bag needs as many ids as bags (%lld ids, %lld bags)",
+                static_cast<long long>(n), static_cast<long long>(bags));
   if (bags == 0) return FLARE_OK;
   int st = FLARE_OK;
   int *err = device_error_word(&st);
   if (!err) return st;
   PooledArgs a{};
   a.table_major = layout == FLARE_LAYOUT_TABLE_MAJOR ? 1 : 0;
+  a.one_id = (one_id && a.table_major) ? 1 : 0;  // ignored with sample-major rows, as in the dedup
   a.table = table;
   a.table_rows = table_rows;
   a.dim = dim;

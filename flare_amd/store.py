@@ -940,8 +940,9 @@ class PooledStepPlan:
         self._id_code = _native.INT32 if self.ids.dtype == torch.int32 else _native.INT64
         self._stream = int(shard.stream.cuda_stream)
         self._dedup_stream: torch.cuda.Stream | None = None
-        # one id per bag (offsets 0, 1, 2, ...) in table-major order: the dedup is told, so that
-        # it keeps no gradient row per occurrence (it checks the claim on the device)
+        # one id per bag (offsets 0, 1, 2, ...) in table-major order: the dedup and the forward are
+        # told, so that the dedup keeps no gradient row per occurrence and the forward reads each
+        # bag's id with its offsets (both check the claim on the device)
         self._dedup_layout = shard._layout_code
         bags = self.batch * shard.num_tables
         if shard.layout == "table_major" and self.n == bags and bags > 0:
@@ -991,7 +992,7 @@ class PooledStepPlan:
         _native.call(
             "flare_gather_pooled_csr", s.state.table.data_ptr(), storage_code(s.state.table.dtype),
             s.total_rows, s.dim, self.ids.data_ptr(), self._id_code, self.n, self.offsets.data_ptr(),
-            s.num_tables, self.batch, s.row_base.data_ptr(), _POOLING[self.pooling], s._layout_code,
+            s.num_tables, self.batch, s.row_base.data_ptr(), _POOLING[self.pooling], self._dedup_layout,
             None if self.weights is None else self.weights.data_ptr(), self.pooled.data_ptr(),
             self._stream,
         )

@@ -65,8 +65,8 @@ typedef enum flare_layout {
    * one id (offsets[k] == k).  Occurrence i is then pooled row i, so the
    * dedup neither stores nor sorts a gradient row per occurrence.  The dedup
    * checks the statement: any bag of another length sets error bit 1 and
-   * rejects the batch (no runs, the update does nothing).  Ignored with
-   * SAMPLE_MAJOR; the pooled gather takes the plain layout values only. */
+   * rejects the batch (no runs, the update does nothing).  Also taken by
+   * flare_gather_pooled_csr.  Ignored with SAMPLE_MAJOR. */
   FLARE_LAYOUT_ONE_ID_PER_BAG = 0x100
 } flare_layout;
 
@@ -132,7 +132,10 @@ int flare_gather_pooled(const void *emb, int32_t value_dtype, int64_t emb_rows,
  * row_base[t]) contribute nothing.  n = number of ids; offsets are clamped
  * to [0, n] (offsets must start at 0, end at n and not decrease; a violation
  * sets the device error word).  out: [batch, num_tables, dim] for
- * FLARE_LAYOUT_SAMPLE_MAJOR, [num_tables, batch, dim] for _TABLE_MAJOR. */
+ * FLARE_LAYOUT_SAMPLE_MAJOR, [num_tables, batch, dim] for _TABLE_MAJOR.
+ * _TABLE_MAJOR | FLARE_LAYOUT_ONE_ID_PER_BAG (n == batch * num_tables) reads
+ * each bag's id without waiting for its offsets; a bag whose offsets are not
+ * (k, k + 1) sets error bit 1 and its row is zeros. */
 int flare_gather_pooled_csr(const void *table, int32_t value_dtype,
                             int64_t table_rows, int32_t dim, const void *ids,
                             int32_t id_dtype, int64_t n, const int64_t *offsets,

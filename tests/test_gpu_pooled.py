@@ -559,3 +559,84 @@ def test_one_id_per_bag_claim_is_checked(gpu_device, no_device_errors):
     assert int(count.item()) == 0
     assert torch.equal(shard.table, table0)
     no_device_errors(1)
+
+
+def _one_id_forward(shard, ids, offsets, batch, pooling, weights, layout_flags):
+    from flare_amd import _native
+    from flare_amd.conversion import storage_code
+
+    dev = shard.device
+    d_ids = torch.from_numpy(ids).to(dev)
+    d_off = torch.from_numpy(offsets).to(dev)
+    d_w = None if weights is None else torch.from_numpy(weights).to(dev)
+    out = torch.full((shard.num_tables, batch, shard.dim), 7.0, dtype=shard.table.dtype, device=dev)
+    code = {"sum": 0, "mean": 1, "weighted": 2}[pooling]
+    id_code = _native.INT32 if ids.dtype == np.int32 else _native.INT64
+    _native.call("flare_gather_pooled_csr", shard.table.data_ptr(), storage_code(shard.table.dtype),
+                 shard.total_rows, shard.dim, d_ids.data_ptr(), id_code, int(ids.size), d_off.data_ptr(),
+                 shard.num_tables, batch, shard.row_base.data_ptr(), code, layout_flags,
+                 None if d_w is None else d_w.data_ptr(), out.data_ptr(),
+                 int(torch.cuda.current_stream(dev).cuda_stream))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("pooling", ["sum", "mean", "weighted"])
+@pytest.mark.parametrize("storage", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("width", [0, 1, 2, 3, 4])
+def test_one_id_forward_bit_exact(gpu_device, no_device_errors, pooling, storage, width):
+    """flare_gather_pooled_csr with the one-id-per-bag flag (ids read with their offsets): rows of
+    4 to 128 16-byte vectors, int32 and int64 ids, some ids past their table (error bit 1, a zero
+    row); every row equals the oracle's pooling of the bag's valid ids."""
+    from flare_amd import _native
+    from flare_amd.store import PooledTableShard, Uniform
+
+    dim = SHORT_DIMS[storage][width]
+    rng = np.random.default_rng(31 + width)
+    table_rows, batch = [9, 300, 41], 1001
+    limit = np.repeat(np.asarray(table_rows), batch)
+    ids = rng.integers(0, 1 << 30, size=limit.size) % limit
+    bad = np.zeros(ids.size, bool)
+    bad[2::53] = True
+    ids = np.where(bad, limit + rng.integers(0, 4, size=ids.size), ids).astype(np.int64)
+    offsets = np.arange(ids.size + 1, dtype=np.int64)
+    weights = rng.uniform(0, 1, size=ids.size).astype(np.float32) if pooling == "weighted" else None
+    shard = PooledTableShard(table_rows, dim, value_dtype=storage, initializer=Uniform(-1.0, 1.0), seed=width,
+                             layout="table_major")
+    flags = _native.LAYOUT_TABLE_MAJOR | _native.LAYOUT_ONE_ID_PER_BAG
+    pooled = _one_id_forward(shard, ids.astype(np.int32) if width == 1 else ids, offsets, batch, pooling,
+                             weights, flags)
+    keep_off = np.zeros(ids.size + 1, np.int64)
+    keep_off[1:] = np.cumsum(~bad)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    expected = O.gather_pooled_csr(_host(shard.table), ids[~bad], keep_off, row_base, batch, dim,
+                                   storage=storage, pooling=pooling,
+                                   weights=None if weights is None else weights[~bad])
+    np.testing.assert_array_equal(_host(pooled), np.ascontiguousarray(expected.transpose(1, 0, 2)))
+    no_device_errors(1)
+
+
+def test_one_id_forward_claim_is_checked(gpu_device, no_device_errors):
+    """The flag with as many ids as bags but one bag of two ids (and so one empty bag): error bit
+    1, the rows of those bags are zeros, every other row is its id's row; the flag with a
+    different id count is refused on the host."""
+    from flare_amd import _native
+    from flare_amd.store import PooledTableShard, Uniform
+
+    shard = PooledTableShard([20, 30], 16, value_dtype="float32", initializer=Uniform(-1.0, 1.0), seed=4,
+                             layout="table_major")
+    batch = 4
+    offsets = np.array([0, 1, 3, 3, 4, 5, 6, 7, 8], np.int64)  # bag 1 holds 2 ids, bag 2 none
+    ids = np.array([1, 2, 3, 4, 5, 6, 7, 8], np.int64)
+    flags = _native.LAYOUT_TABLE_MAJOR | _native.LAYOUT_ONE_ID_PER_BAG
+    pooled = _one_id_forward(shard, ids, offsets, batch, "sum", None, flags).cpu().numpy().reshape(8, 16)
+    table = shard.table.cpu().numpy()
+    base = [0, 0, 0, 0, 20, 20, 20, 20]
+    for k in range(8):
+        if k in (1, 2):
+            np.testing.assert_array_equal(pooled[k], np.zeros(16, np.float32))
+        else:
+            np.testing.assert_array_equal(pooled[k], table[base[k] + ids[k]])
+    no_device_errors(1)
+    with pytest.raises(ValueError):
+        _one_id_forward(shard, ids[:7], offsets[:8], batch, "sum", None, flags)
