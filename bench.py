@@ -712,6 +712,81 @@ def keymap_main(args) -> int:
     return 0
 
 
+def dynamic_main(args) -> int:
+    """The pooled step over int64 keys (DynamicEmbeddingStore): workload 2's ids mixed into
+    arbitrary int64 keys, one 128-wide bf16 table with row-wise Adagrad shared by the 26
+    features.  A step is lookup_pooled (key map lookup_or_insert of every occurrence, then the
+    pooled gather) and apply_pooled_gradients (key map lookup, dedup, segment sums, update)."""
+    import numpy as np
+    import torch
+
+    from flare_amd import _native
+    from flare_amd.store import DynamicEmbeddingStore, RowWiseAdagrad, Uniform
+    from flare_amd.workload import make_workload
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    batches = max(2, min(args.batches, 4))
+    sets = []
+    for k in range(batches):
+        w = make_workload(2, batch_index=k)
+        g = w.global_keys().astype(np.uint64)
+        with np.errstate(over="ignore"):
+            z = (g ^ (g >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+            z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+            z = z ^ (z >> np.uint64(31))
+        keys = z.view(np.int64)
+        keys = np.where(keys == np.iinfo(np.int64).min, 0, keys)
+        sets.append((torch.from_numpy(keys).to(device), torch.from_numpy(w.offsets).to(device)))
+    batch, features, dim = w.batch, w.num_tables, w.dim
+    total = len(torch.unique(torch.cat([k for k, _ in sets])))
+    store = DynamicEmbeddingStore(total + 4096, [dim], value_dtype="bfloat16",
+                                  optimizer=RowWiseAdagrad(lr=0.01, eps=1e-8), initializer=Uniform(-0.01, 0.01),
+                                  seed=5)
+    grad = torch.empty((features, batch, dim), dtype=torch.float32, device=device).normal_(0, 1e-3)
+    grad = grad.to(torch.bfloat16)
+    stream = store.stream
+
+    def step(i):
+        keys, offsets = sets[i % batches]
+        store.lookup_pooled(keys, offsets, batch, dim)
+        store.apply_pooled_gradients(keys, offsets, batch, grad, dim)
+
+    for i in range(max(args.warmup, batches)):
+        step(i)
+    torch.cuda.synchronize()
+    lib = _native.library()
+    lib.flare_take_device_errors(int(stream.cuda_stream))
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            keys, offsets = sets[i % batches]
+            events[i][0].record(stream)
+            store.lookup_pooled(keys, offsets, batch, dim)
+            events[i][1].record(stream)
+            store.apply_pooled_gradients(keys, offsets, batch, grad, dim)
+            events[i][2].record(stream)
+    torch.cuda.synchronize()
+    errors = int(lib.flare_take_device_errors(int(stream.cuda_stream)))
+    fwd = statistics.median(e[0].elapsed_time(e[1]) for e in events)
+    bwd = statistics.median(e[1].elapsed_time(e[2]) for e in events)
+    ms = statistics.median(e[0].elapsed_time(e[2]) for e in events)
+    rows = features * batch
+    print(json.dumps({
+        "metric": "pooled embedding rows/sec (fwd+bwd+update) over int64 keys (dynamic store)",
+        "value": rows / (ms * 1e-3), "unit": "pooled rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "dtype": "f32 (bf16 rows, bf16 pooled grads)",
+        "data": "synthetic (workload 2 ids mixed by splitmix64 into int64 keys, N(0,1e-3) pooled grads)",
+        "config": {"workload": "26 features x batch 65536, one int64 key per bag, one 128-wide bf16 table "
+                               f"of {store.tables[dim].rows} rows with row-wise Adagrad, key map of "
+                               f"{store.maps[dim].slots} slots", "keys_stored": store.size(dim),
+                   "rotated_batches": batches},
+        "phases_ms": {"lookup_pooled": fwd, "apply_pooled_gradients": bwd},
+        "device_errors": errors,
+    }), flush=True)
+    return 0 if errors == 0 else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -741,6 +816,8 @@ def main() -> int:
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
                     help="measure the dynamic store's key map (lookup_or_insert) instead of the pooled step")
+    ap.add_argument("--dynamic", action="store_true",
+                    help="measure the pooled step over int64 keys through the dynamic store instead")
     ap.add_argument("--ingest", action="store_true",
                     help="measure CSR-native ingest (nested global positions) instead of the pooled step")
     ap.add_argument("--row-gather", action="store_true",
@@ -758,6 +835,8 @@ def main() -> int:
 
     if args.keymap:
         return keymap_main(args)
+    if args.dynamic:
+        return dynamic_main(args)
     if args.ingest:
         return ingest_main(args)
     if args.pages:

@@ -701,6 +701,130 @@ class DynamicEmbeddingStore(EmbeddingStore):
             rows = self._resolve(k, int(g.shape[1]), False, values=False)[0].to(torch.int64)
         super().accumulate_gradients(rows, g)
 
+    # -- the fused pooled step over keys ----------------------------------------
+    # The reference materializes one feature group as keys -> unique keys ->
+    # lookup_or_insert of the unique keys (dynamic_embedding.py:397-399) ->
+    # gather_pooled of the compact rows by the padded inverse
+    # (materialization.py:36-79), and on the way back scatter_pooled -> keyed sums
+    # -> accumulate_gradients + optimizer_step (dynamic_embedding.py:481-549).
+    # Here every occurrence's key goes through the key map once (rows in
+    # first-occurrence order, new rows initialised), and the rows feed the fused
+    # CSR kernels over this dim's table directly: T features of B bags, bag
+    # k = t*B + b, pooled rows [T, B, D] (the [B, 1, D] outputs of T
+    # single-feature groups, one after the other).
+    def _pooled_keys(self, keys: Any, offsets: Any, batch_size: int, dim: int):
+        table = self._table(dim)
+        batch_size = int(batch_size)
+        k = self._keys(keys)
+        off = contiguous(to_device(offsets, self.device).reshape(-1).to(torch.int64))
+        if batch_size <= 0 or (off.numel() - 1) % batch_size != 0 or off.numel() < 2:
+            raise ValueError(f"offsets must hold features * batch_size + 1 entries, got {off.numel()} "
+                             f"for batch_size {batch_size}")
+        return table, k, off, (off.numel() - 1) // batch_size
+
+    def _pooled_weights(self, pooling: str, per_sample_weights: Any, n: int):
+        if pooling not in _POOLING:
+            raise ValueError(f"pooling must be one of {sorted(_POOLING)}, got {pooling!r}")
+        if pooling != "weighted":
+            return None
+        if per_sample_weights is None:
+            raise ValueError("weighted pooling requires per_sample_weights")
+        w = contiguous(to_device(per_sample_weights, self.device).reshape(-1).to(torch.float32))
+        if w.numel() != n:
+            raise ValueError("per_sample_weights must have one weight per key")
+        return w
+
+    def _one_table(self, table: _TableState) -> torch.Tensor:
+        """row_base of the whole table as one CSR table: [0, rows] (kept until the table grows)."""
+        cache = self.__dict__.setdefault("_row_bases", {})
+        hit = cache.get(table.dim)
+        if hit is None or hit[0] != table.rows:
+            base = torch.tensor([0, table.rows], dtype=torch.int64).pin_memory()
+            hit = (table.rows, base.to(self.device, non_blocking=True))
+            cache[table.dim] = hit
+        return hit[1]
+
+    def lookup_pooled(self, keys: Any, offsets: Any, batch_size: int, dim: int, *, pooling: str = "sum",
+                      per_sample_weights: Any = None) -> torch.Tensor:
+        """Forward over keys: ``lookup_or_insert`` of every key of the CSR bags, then the pooled
+        gather of their rows; ``[features, batch_size, dim]`` in the value dtype."""
+        with _Ordered(self.stream, self.device) as order:
+            table, k, off, features = self._pooled_keys(keys, offsets, batch_size, dim)
+            n = int(k.numel())
+            w = self._pooled_weights(pooling, per_sample_weights, n)
+            order.hold(k, off, w)
+            rows = self._resolve(k, dim, True, values=False)[0] if n else \
+                torch.empty(1, dtype=torch.int32, device=self.device)
+            out = torch.empty((features, int(batch_size), table.dim), dtype=table.table.dtype, device=self.device)
+            row_base = self._one_table(table)
+            _native.call(
+                "flare_gather_pooled_csr", table.table.data_ptr(), storage_code(table.table.dtype), table.rows,
+                table.dim, rows.data_ptr(), _native.INT32, n, off.data_ptr(), 1, features * int(batch_size),
+                row_base.data_ptr(), _POOLING[pooling], _native.LAYOUT_TABLE_MAJOR,
+                None if w is None else w.data_ptr(), out.data_ptr(), int(self.stream.cuda_stream),
+            )
+            order.give(out)
+        return out
+
+    def apply_pooled_gradients(self, keys: Any, offsets: Any, batch_size: int, pooled_grad: Any, dim: int, *,
+                               pooling: str = "sum", per_sample_weights: Any = None,
+                               normalization_steps: int = 1, return_dedup: bool = False,
+                               validate_values: bool = False):
+        """Backward + update over keys: the rows of the keys (looked up, not inserted: keys without
+        a row set device error bit 1 and are left out), then the fused dedup, deterministic
+        segment sum and optimizer update of this dim's table.  ``pooled_grad``: float32 or
+        bfloat16 ``[features, batch_size, dim]``.  With ``return_dedup`` also returns
+        ``(unique_keys, inverse, first_indices)`` in first-occurrence order (synchronizes)."""
+        if isinstance(normalization_steps, bool) or not isinstance(normalization_steps, int) or \
+                normalization_steps <= 0:
+            raise ValueError("normalization_steps must be a positive integer")
+        with _Ordered(self.stream, self.device) as order:
+            table, k, off, features = self._pooled_keys(keys, offsets, batch_size, dim)
+            n = int(k.numel())
+            w = self._pooled_weights(pooling, per_sample_weights, n)
+            g = _transport_grad(to_device(pooled_grad, self.device))
+            order.hold(k, off, w, g)
+            bags = features * int(batch_size)
+            if g.numel() != bags * table.dim or not g.is_contiguous():
+                raise ValueError(f"pooled gradient must be a contiguous [{features}, {batch_size}, {table.dim}] "
+                                 "tensor")
+            rows = self._resolve(k, dim, False, values=False)[0] if n else \
+                torch.empty(1, dtype=torch.int32, device=self.device)
+            row_base = self._one_table(table)
+            m = max(n, 1)
+            unique = torch.empty(m, dtype=torch.int64, device=self.device)
+            first = torch.empty(m, dtype=torch.int64, device=self.device)
+            inverse = torch.empty(m, dtype=torch.int32, device=self.device)
+            count = torch.zeros(1, dtype=torch.int64, device=self.device)
+            flag = torch.zeros(1, dtype=torch.int32, device=self.device) if validate_values else None
+            nbytes = _native.library().flare_pooled_backward_workspace_bytes(n, table.rows, table.dim)
+            ws = self._workspace.get(nbytes)
+            s0, s1, st = table.pointers()
+            stream = int(self.stream.cuda_stream)
+            _native.call(
+                "flare_pooled_dedup", rows.data_ptr(), _native.INT32, n, off.data_ptr(), 1, bags,
+                row_base.data_ptr(), table.rows, table.dim, _POOLING[pooling], _native.LAYOUT_TABLE_MAJOR,
+                unique.data_ptr(), first.data_ptr(), count.data_ptr(), ws.data_ptr(), nbytes, stream,
+            )
+            _native.call(
+                "flare_pooled_apply_ex", table.table.data_ptr(), storage_code(table.table.dtype), table.rows,
+                table.dim, s0, s1, st, ctypes.byref(table.native_optimizer), n, 1, bags, _POOLING[pooling],
+                None if w is None else w.data_ptr(), g.data_ptr(), _GRAD_TRANSPORT[g.dtype],
+                1 if validate_values else 0, None if flag is None else flag.data_ptr(), int(normalization_steps),
+                None, inverse.data_ptr(), ws.data_ptr(), nbytes, stream,
+            )
+            order.give(inverse, first)
+        if flag is not None:
+            _raise_if_nonfinite(flag, self.stream)
+        if not return_dedup:
+            return None
+        self.stream.synchronize()  # the unique count is read on the host
+        u = int(count.item())
+        first = first[:u]
+        unique_keys = k[first] if u else k[:0]
+        return unique_keys, inverse[:n], first
+
+
 
 # ----------------------------------------------------------------------------
 # PooledTableShard: the fused forward / backward hot path over T tables
