@@ -403,6 +403,73 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_csr_kernel(
   flush_histograms(s_hist, hist, passes, digit);
 }
 
+// Keys of bags of exactly one id in table-major order (the caller's
+// FLARE_LAYOUT_ONE_ID_PER_BAG, n == bags): occurrence i is bag i of table
+// i / batch, so no bag boundaries are staged or searched.  Four consecutive
+// occurrences per thread; the claim is checked as offsets[i] == i for every
+// i <= n (otherwise error bit 1 and the batch is rejected, as in
+// prepare_csr_kernel).  Mean pooling divides by a bag length of 1.
+constexpr int kPrepOneItems = 4;
+
+template <typename IdT>
+__global__ __launch_bounds__(kPrepThreads) void prepare_one_kernel(
+    const IdT *__restrict__ ids, uint32_t n, const int64_t *__restrict__ offsets,
+    const int64_t *__restrict__ row_base, uint32_t batch, int64_t key_limit, int passes, int digit,
+    uint32_t *__restrict__ keys, float *__restrict__ aux, uint32_t *__restrict__ hist,
+    uint32_t *__restrict__ reject, uint32_t *__restrict__ ident_flag, int *err) {
+  __shared__ uint32_t s_hist[kMaxHistBins];
+  for (int i = threadIdx.x; i < (passes << digit); i += kPrepThreads) s_hist[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *ident_flag = 1;
+  __syncthreads();
+  const uint32_t i0 = (blockIdx.x * kPrepThreads + threadIdx.x) * kPrepOneItems;
+  const uint32_t sentinel = static_cast<uint32_t>(key_limit);
+  if (i0 < n) {
+    IdT id[kPrepOneItems];
+    int64_t off[kPrepOneItems];
+#pragma unroll
+    for (int k = 0; k < kPrepOneItems; ++k) {
+      const uint32_t i = i0 + k;
+      id[k] = i < n ? ids[i] : IdT(0);
+      off[k] = i < n ? offsets[i] : 0;
+    }
+    bool claim = true;
+#pragma unroll
+    for (int k = 0; k < kPrepOneItems; ++k)
+      if (i0 + k < n && off[k] != static_cast<int64_t>(i0 + k)) claim = false;
+    if (i0 + kPrepOneItems >= n && i0 <= n && offsets[n] != static_cast<int64_t>(n)) claim = false;
+    if (!claim) {
+      record_error(err, kErrIndexOutOfRange);
+      *reject = 1;
+    }
+    uint32_t key[kPrepOneItems];
+#pragma unroll
+    for (int k = 0; k < kPrepOneItems; ++k) {
+      const uint32_t i = i0 + k;
+      key[k] = sentinel;
+      if (i >= n) continue;
+      const uint32_t t = i / batch;
+      const int64_t lo = row_base[t];
+      const int64_t v = static_cast<int64_t>(id[k]);
+      if (v >= 0 && v < row_base[t + 1] - lo) {
+        key[k] = static_cast<uint32_t>(lo + v);
+      } else {
+        record_error(err, kErrIndexOutOfRange);
+      }
+      add_histograms(s_hist, key[k], passes, digit);
+      if (aux) aux[i] = 1.0f;
+    }
+    if (i0 + kPrepOneItems <= n) {
+      *reinterpret_cast<uint4 *>(keys + i0) = make_uint4(key[0], key[1], key[2], key[3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kPrepOneItems; ++k)
+        if (i0 + k < n) keys[i0 + k] = key[k];
+    }
+  }
+  __syncthreads();
+  flush_histograms(s_hist, hist, passes, digit);
+}
+
 // Keys for generic dedup: (value - minimum) as unsigned, 32 or 64 bits.
 template <typename SrcT, typename K>
 __global__ __launch_bounds__(256) void prepare_generic_kernel(const SrcT *__restrict__ src,
@@ -1492,7 +1559,19 @@ extern "C" int flare_pooled_dedup(const void *ids, int32_t id_dtype, int64_t n,
   const int per_bag = n <= kPerBagLength * bags ? 1 : 0;
   const int pgrid = static_cast<int>(ceil_div(bags, bpb));
   float *aux = pooling == FLARE_POOL_MEAN ? w.aux : nullptr;
-  if (id_dtype == FLARE_INT32)
+  if (one_id && table_major && n == bags) {
+    const int ogrid = static_cast<int>(ceil_div(n, static_cast<int64_t>(kPrepThreads) * kPrepOneItems));
+    if (id_dtype == FLARE_INT32)
+      prepare_one_kernel<int32_t><<<ogrid, kPrepThreads, 0, s>>>(
+          static_cast<const int32_t *>(ids), static_cast<uint32_t>(n), offsets, row_base,
+          static_cast<uint32_t>(batch), rows, plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), aux,
+          w.hist, w.meta + 3, w.meta + 6, err);
+    else
+      prepare_one_kernel<int64_t><<<ogrid, kPrepThreads, 0, s>>>(
+          static_cast<const int64_t *>(ids), static_cast<uint32_t>(n), offsets, row_base,
+          static_cast<uint32_t>(batch), rows, plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), aux,
+          w.hist, w.meta + 3, w.meta + 6, err);
+  } else if (id_dtype == FLARE_INT32)
     prepare_csr_kernel<int32_t><<<pgrid, kPrepThreads, 0, s>>>(
         static_cast<const int32_t *>(ids), n, offsets, bags, bpb, row_base, num_tables, batch, rows,
         plan.passes, plan.digit_bits, static_cast<uint32_t *>(w.keys[0]), w.grad_row, aux, w.hist, w.meta + 3, per_bag,
