@@ -241,20 +241,34 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
       ++cur;
     };
 
-    for (int64_t base = 0; base < total; base += G) {
-      int64_t my_row = -1;
-      float my_w = 1.0f;
-      const int64_t vpos = base + lane;
-      if (vpos < total) {
+    // The ids (and weights) of the next G virtual positions are loaded before
+    // the rows of the current ones, so each step of the stream waits for one
+    // memory round trip (its rows), not two (its ids, then their rows).
+    IdT next_id = 0;
+    float next_w = 1.0f;
+    int64_t next_lo = 0, next_rows = 0;
+    bool next_valid = false;
+    auto fetch = [&](int64_t at) {
+      const int64_t vpos = at + lane;
+      next_valid = vpos < total;
+      if (next_valid) {
         int k = 0;  // bag of this virtual position within the group
 #pragma unroll
         for (int j = 1; j < kBagsPerGroup; ++j) k += (vpos >= pre[j]) ? 1 : 0;
         const int lb = lb0 + k;
         const int64_t i = s_begin[lb] + (vpos - pre[k]);
-        const int64_t lo = s_lo[lb];
-        my_row = resolve_row<kCsr, IdT>(a, i, lo, lo + s_rows[lb]);
-        if (weighted) my_w = a.weights[i];
+        next_lo = s_lo[lb];
+        next_rows = s_rows[lb];
+        next_id = static_cast<const IdT *>(a.ids)[i];
+        if (weighted) next_w = a.weights[i];
       }
+    };
+    fetch(0);
+    for (int64_t base = 0; base < total; base += G) {
+      const int64_t my_row =
+          next_valid ? resolve_id<kCsr>(a, static_cast<int64_t>(next_id), next_lo, next_lo + next_rows) : -1;
+      const float my_w = next_w;
+      if (base + G < total) fetch(base + G);
       const int n = (total - base) < G ? static_cast<int>(total - base) : G;
       for (int k = 0; k < n; k += kDepth) {
         R raw[kDepth][L];
