@@ -1028,7 +1028,15 @@ def main() -> int:
     else:
         sums_name = ("piece_sums_kernel", "per-piece sums of keys with several occurrences; one launch per step")
         apply_name = ("key_apply_kernel", "row-wise update of every key; one launch per step")
-    kernels = [roofline("pooled_kernel", "CSR pooled gather, forward; one launch per step", fwd_gbs, fwd_ms, fb0),
+    # the forward kernel the library picks for this batch: one id per bag (table-major plan),
+    # bags of at most 2 ids on average, or the general pooled gather
+    if plans[0]._dedup_layout & _native.LAYOUT_ONE_ID_PER_BAG:
+        fwd_name = ("pooled_one_kernel", "CSR pooled gather of one id per bag, forward; one launch per step")
+    elif w0.num_ids <= 2 * w0.batch * w0.num_tables:
+        fwd_name = ("pooled_short_kernel", "CSR pooled gather of short bags, forward; one launch per step")
+    else:
+        fwd_name = ("pooled_kernel", "CSR pooled gather, forward; one launch per step")
+    kernels = [roofline(*fwd_name, fwd_gbs, fwd_ms, fb0),
                roofline(*sums_name, sums_gbs, sums_ms, sb0),
                roofline(*apply_name, applyk_gbs, applyk_ms, ab0)]
     dominant = max(kernels, key=lambda k: k["kernel_ms"])
