@@ -640,3 +640,53 @@ def test_one_id_forward_claim_is_checked(gpu_device, no_device_errors):
     no_device_errors(1)
     with pytest.raises(ValueError):
         _one_id_forward(shard, ids[:7], offsets[:8], batch, "sum", None, flags)
+
+
+# row widths for the long-bag path: 64 to 512 elements, and 96 / 32 (not multiples of 64)
+LONG_DIMS = {"bfloat16": (64, 128, 256, 512, 96), "float16": (64, 128, 256, 512, 96),
+             "float32": (64, 128, 256, 96, 32)}
+
+
+@pytest.mark.parametrize("layout", ["sample_major", "table_major"])
+@pytest.mark.parametrize("pooling", ["sum", "mean", "weighted"])
+@pytest.mark.parametrize("storage", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("width", [0, 1, 2, 3, 4])
+def test_long_bag_forward_bit_exact(gpu_device, no_device_errors, layout, pooling, storage, width):
+    """Bags of 8-40 ids (a few of 0, 1 and 130-300), so at least 8 per bag on average (the
+    long-bag path: several rounds of prefetched ids per lane-group stream), rows of 32 to 512
+    elements, int32 and int64 ids, both layouts; some ids past their table (error bit 1, pooled
+    as absent); against the oracle, bit for bit."""
+    from flare_amd.store import PooledTableShard, Uniform
+
+    dim = LONG_DIMS[storage][width]
+    rng = np.random.default_rng(41 + width)
+    table_rows, batch = [13, 700, 90], 97
+    lengths = rng.integers(8, 41, size=len(table_rows) * batch)
+    lengths[3::29] = 0
+    lengths[7::31] = 1
+    lengths[11::50] = rng.integers(130, 301, size=lengths[11::50].size)
+    offsets = np.zeros(lengths.size + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    assert offsets[-1] >= 8 * lengths.size
+    bag_table = np.repeat(np.arange(lengths.size) // batch, lengths)
+    limit = np.asarray(table_rows)[bag_table]
+    ids = rng.integers(0, 1 << 30, size=int(offsets[-1])) % limit
+    bad = np.zeros(ids.size, bool)
+    bad[5::67] = True
+    ids = np.where(bad, limit + rng.integers(0, 3, size=ids.size), ids).astype(np.int64)
+    weights = rng.uniform(0, 1, size=ids.size).astype(np.float32) if pooling == "weighted" else None
+    shard = PooledTableShard(table_rows, dim, value_dtype=storage, initializer=Uniform(-1.0, 1.0), seed=width,
+                             layout=layout)
+    pooled = shard.lookup_pooled(ids.astype(np.int32) if width == 1 else ids, offsets, batch, pooling=pooling,
+                                 per_sample_weights=weights)
+    shard.synchronize()
+    keep_len = np.add.reduceat(~bad, offsets[:-1]) * (lengths > 0)
+    keep_off = np.zeros(lengths.size + 1, np.int64)
+    keep_off[1:] = np.cumsum(keep_len)
+    row_base = np.concatenate([[0], np.cumsum(table_rows)]).astype(np.int64)
+    expected = O.gather_pooled_csr(_host(shard.table), ids[~bad], keep_off, row_base, batch, dim, storage=storage,
+                                   pooling=pooling, weights=None if weights is None else weights[~bad])
+    if layout == "table_major":
+        expected = np.ascontiguousarray(expected.transpose(1, 0, 2))
+    np.testing.assert_array_equal(_host(pooled), expected)
+    no_device_errors(1)
