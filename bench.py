@@ -808,10 +808,13 @@ def main() -> int:
                          "tables (the gradient transport dtype of the reference's BF16 and FP16 precision "
                          "policies, src/flare/jax/training/precision.py:62-69, cast before the gradient "
                          "leaves the JAX worker, train_worker.py:467-474), float32 for float32 tables")
-    ap.add_argument("--order", choices=["dedup-first", "forward-first"], default="forward-first",
-                    help="order of the step's first two phases on one stream: the dedup of the ids and then "
-                         "the pooled gather (the reference's order: unique ids before the lookup, "
-                         "src/flare/runtime/fluxway/workers/sparse_input.py:333-349), or the gather first")
+    ap.add_argument("--order", choices=["pipelined", "dedup-first", "forward-first"], default="pipelined",
+                    help="pipelined: each step runs its forward, then its update on the shard's stream while "
+                         "the next batch's dedup runs on a second stream (the reference computes unique ids in "
+                         "its input worker, ahead of the step: src/flare/runtime/fluxway/workers/"
+                         "sparse_input.py:333-349); a step ends when both are done, so every timed step holds "
+                         "one forward, one dedup and one update.  dedup-first / forward-first: the three "
+                         "phases one after another on one stream")
     ap.add_argument("--overlap", action="store_true",
                     help="run the dedup (ids only) on a second stream, concurrent with the forward")
     ap.add_argument("--keymap", action="store_true",
@@ -903,22 +906,40 @@ def main() -> int:
         log(f"copy calibration: 3 x {args.copy_mib} MiB read + {args.copy_mib} MiB written")
         del src, dst
 
-    def run(p):
-        p.forward()
-        p.dedup()
-        p.apply(grad, grad_out=grad_out, optimizer=none_opt)
-
+    pipelined = args.order == "pipelined" and not args.overlap
+    if pipelined and len(plans) < 2:
+        raise SystemExit("the pipelined order needs at least 2 batches (the next batch's dedup runs beside "
+                         "the current batch's update, each in its own workspace)")
     stream = shard.stream
+    aux = torch.cuda.Stream(device=device)
+
+    def run(i):
+        p = plans[i % len(plans)]
+        if pipelined:
+            # the dedup of plans[i] ran during step i-1 (or before the first step)
+            p.forward()
+            q = plans[(i + 1) % len(plans)]
+            aux.wait_stream(stream)  # plans[i+1]'s workspace is free: its last apply is queued before
+            q._dedup_on(int(aux.cuda_stream))
+            p.apply(grad, grad_out=grad_out, optimizer=none_opt)
+            stream.wait_stream(aux)
+        else:
+            p.forward()
+            p.dedup()
+            p.apply(grad, grad_out=grad_out, optimizer=none_opt)
+
     # every call below is enqueued with the shard's stream current, so the plans order nothing
     stream_ctx = torch.cuda.stream(stream)
     stream_ctx.__enter__()
+    if pipelined:
+        plans[0].dedup()
     for i in range(args.warmup):
-        run(plans[i % len(plans)])
+        run(i)
     shard.synchronize()
     torch.cuda.synchronize()
 
     overlap = args.overlap
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(args.steps)]
     # markers inside the update call, after sums_kernel and after the folds (recorded once
     # here so that each event exists before its handle is taken).  The update call launches
     # nothing before sums_kernel or after apply_kernel, so ev[4] and ev[5] bound those two.
@@ -930,7 +951,6 @@ def main() -> int:
             e.record(stream)
     handles = [(ctypes.c_void_p * 4)(None, mk[0].cuda_event, mk[1].cuda_event, None) for mk in markers]
     lib = _native.library()
-    aux = torch.cuda.Stream(device=device)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     order = []
@@ -941,6 +961,29 @@ def main() -> int:
         order.append(k)
         ev = events[i]
         ev[0].record(stream)
+        if pipelined:
+            # forward; then this batch's update (its dedup ran beside the previous update) while
+            # the next batch's dedup runs on the second stream.  A step lasts from its forward to
+            # the next step's forward; the last one ends when the final dedup is done.
+            p.forward()
+            ev[1].record(stream)
+            if i > 0:
+                stream.wait_event(events[i - 1][3])  # this batch's dedup
+            q = plans[(k + 1) % len(plans)]
+            aux.wait_stream(stream)  # q's workspace is free: its last update is queued before here
+            ev[2].record(aux)
+            q._dedup_on(int(aux.cuda_stream))
+            ev[3].record(aux)
+            ev[4] = ev[1]
+            _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
+            p.apply(grad, grad_out=grad_out, optimizer=none_opt)
+            ev[5].record(stream)
+            if i > 0:
+                events[i - 1][6] = ev[0]
+            if i + 1 == args.steps:
+                stream.wait_event(ev[3])
+                ev[6].record(stream)
+            continue
         if overlap:
             # dedup (ids only) on a second stream, concurrent with the forward
             aux.wait_stream(stream)
@@ -990,7 +1033,7 @@ def main() -> int:
     for i, ev in enumerate(events):
         b = batches[order[i]]
         f = fwd_start[i].elapsed_time(ev[1])
-        t = ev[0].elapsed_time(ev[5])
+        t = ev[0].elapsed_time(ev[6] if pipelined else ev[5])
         a = ev[4].elapsed_time(ev[5])
         step_ms.append(t)
         fwd_ms.append(f)
@@ -1064,8 +1107,10 @@ def main() -> int:
             "unique_per_step": uniques[0],
             "rotated_batches": len(plans),
             "dedup": "concurrent with the forward" if overlap else
-                     ("before the forward, same stream" if args.order == "dedup-first" else
-                      "after the forward, same stream"),
+                     ("one batch ahead: the next batch's dedup on a second stream beside this batch's "
+                      "update; each step ends when both are done" if pipelined else
+                      ("before the forward, same stream" if args.order == "dedup-first" else
+                       "after the forward, same stream")),
             "pooled_layout": "[T, B, D]" if args.layout == "table_major" else "[B, T, D]",
             "pooled_grad_dtype": grad_dtype,
         },
