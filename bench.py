@@ -969,12 +969,14 @@ def main() -> int:
             ev[1].record(stream)
             if i > 0:
                 stream.wait_event(events[i - 1][3])  # this batch's dedup
+                ev[4].record(stream)  # the update starts once its dedup is done
+            else:
+                ev[4] = ev[1]
             q = plans[(k + 1) % len(plans)]
             aux.wait_stream(stream)  # q's workspace is free: its last update is queued before here
             ev[2].record(aux)
             q._dedup_on(int(aux.cuda_stream))
             ev[3].record(aux)
-            ev[4] = ev[1]
             _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
             p.apply(grad, grad_out=grad_out, optimizer=none_opt)
             ev[5].record(stream)

@@ -1167,3 +1167,63 @@ class PooledStepPlan:
         self._leave(caller)
         if validate_values:
             _raise_if_nonfinite(self.nonfinite, s.stream)
+
+
+class PooledStepPipeline:
+    """Training steps over a ring of bound batches, each batch's dedup one step ahead.
+
+    The dedup of a batch needs only its ids, as the reference's input worker computes the
+    unique ids of a batch ahead of the step that consumes it
+    (``src/flare/runtime/fluxway/workers/sparse_input.py:333-349``).  ``step(i, grad)`` runs
+    batch ``i``'s forward on the shard's stream, then its update (after its own dedup) while
+    batch ``i + 1``'s dedup runs on a second stream at the default priority.  Each plan has its
+    own workspace, and a dedup starts only after everything queued before it on the shard's
+    stream, so it never overwrites a workspace an earlier update still reads.  Steps must be
+    taken in order ``0, 1, 2, ...``; ``step`` returns the batch's pooled rows (the forward's
+    output, valid on the shard's stream) and ``finish()`` waits for the last dedup.
+    """
+
+    def __init__(self, plans: Sequence[PooledStepPlan]):
+        if len(plans) < 2:
+            raise ValueError("a pipeline needs at least 2 plans (the next batch's dedup runs beside "
+                             "the current batch's update, each in its own workspace)")
+        shards = {id(p.shard) for p in plans}
+        if len(shards) != 1:
+            raise ValueError("the plans of a pipeline must belong to one shard")
+        self.plans = list(plans)
+        self.shard = self.plans[0].shard
+        self.stream = torch.cuda.Stream(device=self.shard.device)
+        self._next = 0
+        self._ready: torch.cuda.Event | None = None  # dedup of the next step's plan
+
+    def _dedup_ahead(self, plan: PooledStepPlan) -> None:
+        main = self.shard.stream
+        self.stream.wait_stream(main)  # plan's workspace is free: its last update is queued before
+        plan._dedup_on(int(self.stream.cuda_stream))
+        self._ready = torch.cuda.Event()
+        self._ready.record(self.stream)
+
+    def step(self, i: int, pooled_grad: torch.Tensor, normalization_steps: int = 1,
+             grad_out: torch.Tensor | None = None, optimizer: Any = None) -> torch.Tensor:
+        """Forward, then update of plan ``i % len(plans)``, with the next plan's dedup beside it."""
+        if i != self._next:
+            raise ValueError(f"pipeline steps must be taken in order: expected step {self._next}, got {i}")
+        p = self.plans[i % len(self.plans)]
+        main = self.shard.stream
+        caller = p._enter()
+        if self._ready is None:  # first step: this plan's dedup has not run yet
+            p._dedup_on(int(main.cuda_stream))
+        pooled = p.forward()  # does not wait for the dedup still running ahead
+        if self._ready is not None:
+            main.wait_event(self._ready)  # this plan's dedup, run during the previous step
+        self._dedup_ahead(self.plans[(i + 1) % len(self.plans)])
+        p.apply(pooled_grad, normalization_steps, grad_out, optimizer)
+        p._leave(caller)
+        self._next = i + 1
+        return pooled
+
+    def finish(self) -> None:
+        """Make the shard's stream (and the caller's) wait for the dedup still running ahead."""
+        if self._ready is not None:
+            self.shard.stream.wait_event(self._ready)
+            torch.cuda.current_stream(self.shard.device).wait_event(self._ready)

@@ -690,3 +690,57 @@ def test_long_bag_forward_bit_exact(gpu_device, no_device_errors, layout, poolin
         expected = np.ascontiguousarray(expected.transpose(1, 0, 2))
     np.testing.assert_array_equal(_host(pooled), expected)
     no_device_errors(1)
+
+
+@pytest.mark.parametrize("num_plans", [2, 3])
+def test_pipeline_matches_serial_steps(gpu_device, no_device_errors, num_plans):
+    """PooledStepPipeline (each batch's dedup one step ahead, on a second stream beside the
+    previous update) against the same steps run one phase after another on another shard:
+    pooled rows, dedup outputs and the final table and state bit for bit, and the
+    first-step pooled rows against the oracle."""
+    from flare_amd.store import PooledStepPipeline, PooledTableShard, RowWiseAdagrad, Uniform
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    ws = [make_workload(2, batch=900, row_scale=0.0005, batch_index=k) for k in range(num_plans)]
+    w0 = ws[0]
+
+    def shard():
+        return PooledTableShard(w0.table_rows, w0.dim, value_dtype=w0.value_dtype,
+                                optimizer=RowWiseAdagrad(lr=0.05, eps=1e-8), initializer=Uniform(-0.01, 0.01),
+                                seed=21, layout="table_major")
+
+    grads = [torch.from_numpy(np.ascontiguousarray(pooled_grad_host(w).transpose(1, 0, 2))).to(gpu_device)
+             for w in ws]
+    a, b = shard(), shard()
+    table0 = _host(a.table.clone())
+    pa = [a.plan_step(w.ids, w.offsets, w.batch) for w in ws]
+    pb = [b.plan_step(w.ids, w.offsets, w.batch) for w in ws]
+    pipe = PooledStepPipeline(pa)
+    steps = 2 * num_plans + 1
+    for i in range(steps):
+        k = i % num_plans
+        pooled_a = pipe.step(i, grads[k]).clone()
+        pooled_b = pb[k].forward().clone()
+        pb[k].dedup()
+        pb[k].apply(grads[k])
+        a.synchronize()
+        b.synchronize()
+        np.testing.assert_array_equal(_host(pooled_a), _host(pooled_b))
+        u = int(pb[k].unique_count.item())
+        assert int(pa[k].unique_count.item()) == u
+        np.testing.assert_array_equal(pa[k].unique[:u].cpu().numpy(), pb[k].unique[:u].cpu().numpy())
+        np.testing.assert_array_equal(pa[k].inverse[:ws[k].num_ids].cpu().numpy(),
+                                      pb[k].inverse[:ws[k].num_ids].cpu().numpy())
+        if i == 0:
+            e_pooled = O.gather_pooled_csr(table0, w0.ids, w0.offsets, w0.row_base(), w0.batch, w0.dim,
+                                           storage=w0.value_dtype)
+            np.testing.assert_array_equal(_host(pooled_a), np.ascontiguousarray(e_pooled.transpose(1, 0, 2)))
+    pipe.finish()
+    a.synchronize()
+    np.testing.assert_array_equal(_host(a.table), _host(b.table))
+    np.testing.assert_array_equal(a.state.state0.cpu().numpy(), b.state.state0.cpu().numpy())
+    with pytest.raises(ValueError):
+        pipe.step(0, grads[0])
+    with pytest.raises(ValueError):
+        PooledStepPipeline(pa[:1])
+    no_device_errors()
