@@ -852,7 +852,7 @@ def main() -> int:
     import torch
 
     from flare_amd import _native
-    from flare_amd.store import Adam, PooledTableShard, RowWiseAdagrad, Uniform
+    from flare_amd.store import Adam, PooledStepPipeline, PooledTableShard, RowWiseAdagrad, Uniform
     from flare_amd.workload import make_workload
 
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
@@ -911,19 +911,15 @@ def main() -> int:
         raise SystemExit("the pipelined order needs at least 2 batches (the next batch's dedup runs beside "
                          "the current batch's update, each in its own workspace)")
     stream = shard.stream
-    aux = torch.cuda.Stream(device=device)
+    aux = torch.cuda.Stream(device=device)  # --overlap: the dedup beside the forward
+
+    pipe = PooledStepPipeline(plans) if pipelined else None
 
     def run(i):
-        p = plans[i % len(plans)]
         if pipelined:
-            # the dedup of plans[i] ran during step i-1 (or before the first step)
-            p.forward()
-            q = plans[(i + 1) % len(plans)]
-            aux.wait_stream(stream)  # plans[i+1]'s workspace is free: its last apply is queued before
-            q._dedup_on(int(aux.cuda_stream))
-            p.apply(grad, grad_out=grad_out, optimizer=none_opt)
-            stream.wait_stream(aux)
+            pipe.step(i, grad, grad_out=grad_out, optimizer=none_opt)
         else:
+            p = plans[i % len(plans)]
             p.forward()
             p.dedup()
             p.apply(grad, grad_out=grad_out, optimizer=none_opt)
@@ -931,8 +927,6 @@ def main() -> int:
     # every call below is enqueued with the shard's stream current, so the plans order nothing
     stream_ctx = torch.cuda.stream(stream)
     stream_ctx.__enter__()
-    if pipelined:
-        plans[0].dedup()
     for i in range(args.warmup):
         run(i)
     shard.synchronize()
@@ -962,28 +956,19 @@ def main() -> int:
         ev = events[i]
         ev[0].record(stream)
         if pipelined:
-            # forward; then this batch's update (its dedup ran beside the previous update) while
-            # the next batch's dedup runs on the second stream.  A step lasts from its forward to
-            # the next step's forward; the last one ends when the final dedup is done.
-            p.forward()
-            ev[1].record(stream)
-            if i > 0:
-                stream.wait_event(events[i - 1][3])  # this batch's dedup
-                ev[4].record(stream)  # the update starts once its dedup is done
-            else:
-                ev[4] = ev[1]
-            q = plans[(k + 1) % len(plans)]
-            aux.wait_stream(stream)  # q's workspace is free: its last update is queued before here
-            ev[2].record(aux)
-            q._dedup_on(int(aux.cuda_stream))
-            ev[3].record(aux)
+            # PooledStepPipeline: forward; then this batch's update (its dedup ran beside the
+            # previous update) while the next batch's dedup runs on the pipeline's stream.  A step
+            # lasts from its forward to the next step's forward; the last one ends when the final
+            # dedup is done.
+            marks = dict.fromkeys(("forward_done", "update_start", "dedup_start", "dedup_done", "update_done"))
             _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
-            p.apply(grad, grad_out=grad_out, optimizer=none_opt)
-            ev[5].record(stream)
+            pipe.step(args.warmup + i, grad, grad_out=grad_out, optimizer=none_opt, marks=marks)
+            ev[1], ev[4], ev[2], ev[3], ev[5] = (marks["forward_done"], marks["update_start"], marks["dedup_start"],
+                                                 marks["dedup_done"], marks["update_done"])
             if i > 0:
                 events[i - 1][6] = ev[0]
             if i + 1 == args.steps:
-                stream.wait_event(ev[3])
+                pipe.finish()
                 ev[6].record(stream)
             continue
         if overlap:

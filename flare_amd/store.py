@@ -1169,6 +1169,14 @@ class PooledStepPlan:
             _raise_if_nonfinite(self.nonfinite, s.stream)
 
 
+def _mark(marks: dict, key: str, stream: torch.cuda.Stream) -> None:
+    """Record a timing event under ``key`` when the caller asked for that phase boundary."""
+    if key in marks:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        marks[key] = ev
+
+
 class PooledStepPipeline:
     """Training steps over a ring of bound batches, each batch's dedup one step ahead.
 
@@ -1196,28 +1204,42 @@ class PooledStepPipeline:
         self._next = 0
         self._ready: torch.cuda.Event | None = None  # dedup of the next step's plan
 
-    def _dedup_ahead(self, plan: PooledStepPlan) -> None:
+    def _dedup_ahead(self, plan: PooledStepPlan, marks: dict) -> None:
         main = self.shard.stream
         self.stream.wait_stream(main)  # plan's workspace is free: its last update is queued before
+        _mark(marks, "dedup_start", self.stream)
         plan._dedup_on(int(self.stream.cuda_stream))
-        self._ready = torch.cuda.Event()
+        self._ready = torch.cuda.Event(enable_timing="dedup_done" in marks)
         self._ready.record(self.stream)
+        if "dedup_done" in marks:
+            marks["dedup_done"] = self._ready
 
     def step(self, i: int, pooled_grad: torch.Tensor, normalization_steps: int = 1,
-             grad_out: torch.Tensor | None = None, optimizer: Any = None) -> torch.Tensor:
-        """Forward, then update of plan ``i % len(plans)``, with the next plan's dedup beside it."""
+             grad_out: torch.Tensor | None = None, optimizer: Any = None,
+             marks: dict | None = None) -> torch.Tensor:
+        """Forward, then update of plan ``i % len(plans)``, with the next plan's dedup beside it.
+
+        ``marks`` (optional, for timing): a dict whose keys name phase boundaries to record as
+        timing events -- ``"forward_done"`` and ``"update_start"`` / ``"update_done"`` on the
+        shard's stream, ``"dedup_start"`` / ``"dedup_done"`` (the next batch's dedup) on the
+        pipeline's stream.  Each recorded event is stored under its key.
+        """
         if i != self._next:
             raise ValueError(f"pipeline steps must be taken in order: expected step {self._next}, got {i}")
+        marks = {} if marks is None else marks
         p = self.plans[i % len(self.plans)]
         main = self.shard.stream
         caller = p._enter()
         if self._ready is None:  # first step: this plan's dedup has not run yet
             p._dedup_on(int(main.cuda_stream))
         pooled = p.forward()  # does not wait for the dedup still running ahead
+        _mark(marks, "forward_done", main)
         if self._ready is not None:
             main.wait_event(self._ready)  # this plan's dedup, run during the previous step
-        self._dedup_ahead(self.plans[(i + 1) % len(self.plans)])
+        _mark(marks, "update_start", main)
+        self._dedup_ahead(self.plans[(i + 1) % len(self.plans)], marks)
         p.apply(pooled_grad, normalization_steps, grad_out, optimizer)
+        _mark(marks, "update_done", main)
         p._leave(caller)
         self._next = i + 1
         return pooled
