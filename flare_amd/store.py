@@ -1182,13 +1182,14 @@ class PooledStepPipeline:
 
     The dedup of a batch needs only its ids, as the reference's input worker computes the
     unique ids of a batch ahead of the step that consumes it
-    (``src/flare/runtime/fluxway/workers/sparse_input.py:333-349``).  ``step(i, grad)`` runs
-    batch ``i``'s forward on the shard's stream, then its update (after its own dedup) while
-    batch ``i + 1``'s dedup runs on a second stream at the default priority.  Each plan has its
-    own workspace, and a dedup starts only after everything queued before it on the shard's
-    stream, so it never overwrites a workspace an earlier update still reads.  Steps must be
-    taken in order ``0, 1, 2, ...``; ``step`` returns the batch's pooled rows (the forward's
-    output, valid on the shard's stream) and ``finish()`` waits for the last dedup.
+    (``src/flare/runtime/fluxway/workers/sparse_input.py:333-349``).  ``forward(i)`` pools
+    batch ``i`` on the shard's stream and queues batch ``i + 1``'s dedup on a second stream
+    (default priority), where it runs while the caller's dense network and batch ``i``'s update
+    run; ``update(i, grad)`` waits for batch ``i``'s own dedup and applies the update.  Each
+    plan has its own workspace, and a dedup starts only after everything queued before it on
+    the shard's stream, so it never overwrites a workspace an earlier update still reads.
+    Steps go in order ``0, 1, 2, ...``, each ``forward`` followed by its ``update``;
+    ``finish()`` waits for the dedup still running ahead.
     """
 
     def __init__(self, plans: Sequence[PooledStepPlan]):
@@ -1201,51 +1202,77 @@ class PooledStepPipeline:
         self.plans = list(plans)
         self.shard = self.plans[0].shard
         self.stream = torch.cuda.Stream(device=self.shard.device)
-        self._next = 0
-        self._ready: torch.cuda.Event | None = None  # dedup of the next step's plan
+        self._next = 0  # the step whose forward comes next
+        self._pending: int | None = None  # the step whose update comes next
+        self._ready: dict[int, torch.cuda.Event] = {}  # step -> its dedup, run ahead
 
-    def _dedup_ahead(self, plan: PooledStepPlan, marks: dict) -> None:
+    def _plan(self, i: int) -> PooledStepPlan:
+        return self.plans[i % len(self.plans)]
+
+    def forward(self, i: int, marks: dict | None = None) -> torch.Tensor:
+        """Pool batch ``i`` (``plans[i % len(plans)]``) and queue batch ``i + 1``'s dedup.
+
+        ``marks`` (optional, for timing): a dict whose keys name phase boundaries to record as
+        timing events -- ``"forward_done"`` on the shard's stream, ``"dedup_start"`` /
+        ``"dedup_done"`` (batch ``i + 1``'s dedup) on the pipeline's stream.
+        """
+        if i != self._next or self._pending is not None:
+            raise ValueError(f"pipeline steps go in order, each forward followed by its update: "
+                             f"expected forward {self._next}" if self._pending is None else
+                             f"expected update {self._pending} before forward {i}")
+        marks = {} if marks is None else marks
+        p = self._plan(i)
         main = self.shard.stream
-        self.stream.wait_stream(main)  # plan's workspace is free: its last update is queued before
+        caller = p._enter()
+        if i not in self._ready:  # the first step: its dedup has not run ahead
+            p._dedup_on(int(main.cuda_stream))
+        pooled = p.forward()  # does not wait for a dedup still running ahead
+        _mark(marks, "forward_done", main)
+        # batch i+1's plan is free: its last update is queued on the shard's stream before here
+        self.stream.wait_stream(main)
         _mark(marks, "dedup_start", self.stream)
-        plan._dedup_on(int(self.stream.cuda_stream))
-        self._ready = torch.cuda.Event(enable_timing="dedup_done" in marks)
-        self._ready.record(self.stream)
+        self._plan(i + 1)._dedup_on(int(self.stream.cuda_stream))
+        ready = torch.cuda.Event(enable_timing="dedup_done" in marks)
+        ready.record(self.stream)
+        self._ready[i + 1] = ready
         if "dedup_done" in marks:
-            marks["dedup_done"] = self._ready
+            marks["dedup_done"] = ready
+        p._leave(caller)
+        self._pending = i
+        return pooled
+
+    def update(self, i: int, pooled_grad: torch.Tensor, normalization_steps: int = 1,
+               grad_out: torch.Tensor | None = None, optimizer: Any = None,
+               marks: dict | None = None) -> None:
+        """Batch ``i``'s update (``PooledStepPlan.apply``) once its dedup is done.  ``marks``:
+        ``"update_start"`` / ``"update_done"`` on the shard's stream."""
+        if self._pending != i:
+            raise ValueError(f"update {i} without its forward (pending: {self._pending})")
+        marks = {} if marks is None else marks
+        p = self._plan(i)
+        main = self.shard.stream
+        caller = p._enter()
+        ready = self._ready.pop(i, None)
+        if ready is not None:
+            main.wait_event(ready)
+        _mark(marks, "update_start", main)
+        p.apply(pooled_grad, normalization_steps, grad_out, optimizer)
+        _mark(marks, "update_done", main)
+        p._leave(caller)
+        self._pending = None
+        self._next = i + 1
 
     def step(self, i: int, pooled_grad: torch.Tensor, normalization_steps: int = 1,
              grad_out: torch.Tensor | None = None, optimizer: Any = None,
              marks: dict | None = None) -> torch.Tensor:
-        """Forward, then update of plan ``i % len(plans)``, with the next plan's dedup beside it.
-
-        ``marks`` (optional, for timing): a dict whose keys name phase boundaries to record as
-        timing events -- ``"forward_done"`` and ``"update_start"`` / ``"update_done"`` on the
-        shard's stream, ``"dedup_start"`` / ``"dedup_done"`` (the next batch's dedup) on the
-        pipeline's stream.  Each recorded event is stored under its key.
-        """
-        if i != self._next:
-            raise ValueError(f"pipeline steps must be taken in order: expected step {self._next}, got {i}")
-        marks = {} if marks is None else marks
-        p = self.plans[i % len(self.plans)]
-        main = self.shard.stream
-        caller = p._enter()
-        if self._ready is None:  # first step: this plan's dedup has not run yet
-            p._dedup_on(int(main.cuda_stream))
-        pooled = p.forward()  # does not wait for the dedup still running ahead
-        _mark(marks, "forward_done", main)
-        if self._ready is not None:
-            main.wait_event(self._ready)  # this plan's dedup, run during the previous step
-        _mark(marks, "update_start", main)
-        self._dedup_ahead(self.plans[(i + 1) % len(self.plans)], marks)
-        p.apply(pooled_grad, normalization_steps, grad_out, optimizer)
-        _mark(marks, "update_done", main)
-        p._leave(caller)
-        self._next = i + 1
+        """``forward(i)`` then ``update(i, pooled_grad)``: a step whose gradient is known up
+        front (benchmarks, replays)."""
+        pooled = self.forward(i, marks)
+        self.update(i, pooled_grad, normalization_steps, grad_out, optimizer, marks)
         return pooled
 
     def finish(self) -> None:
         """Make the shard's stream (and the caller's) wait for the dedup still running ahead."""
-        if self._ready is not None:
-            self.shard.stream.wait_event(self._ready)
-            torch.cuda.current_stream(self.shard.device).wait_event(self._ready)
+        for ready in self._ready.values():
+            self.shard.stream.wait_event(ready)
+            torch.cuda.current_stream(self.shard.device).wait_event(ready)

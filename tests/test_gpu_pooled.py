@@ -695,7 +695,8 @@ def test_long_bag_forward_bit_exact(gpu_device, no_device_errors, layout, poolin
 @pytest.mark.parametrize("num_plans", [2, 3])
 def test_pipeline_matches_serial_steps(gpu_device, no_device_errors, num_plans):
     """PooledStepPipeline (each batch's dedup one step ahead, on a second stream beside the
-    previous update) against the same steps run one phase after another on another shard:
+    previous update), through step() and through forward() / update(), against the same steps
+    run one phase after another on another shard:
     pooled rows, dedup outputs and the final table and state bit for bit, and the
     first-step pooled rows against the oracle."""
     from flare_amd.store import PooledStepPipeline, PooledTableShard, RowWiseAdagrad, Uniform
@@ -719,7 +720,13 @@ def test_pipeline_matches_serial_steps(gpu_device, no_device_errors, num_plans):
     steps = 2 * num_plans + 1
     for i in range(steps):
         k = i % num_plans
-        pooled_a = pipe.step(i, grads[k]).clone()
+        if i % 2:
+            pooled_a = pipe.step(i, grads[k]).clone()
+        else:  # the training-loop form: the gradient is given after the forward
+            pooled_a = pipe.forward(i).clone()
+            with pytest.raises(ValueError):
+                pipe.forward(i + 1)  # the update of step i comes first
+            pipe.update(i, grads[k])
         pooled_b = pb[k].forward().clone()
         pb[k].dedup()
         pb[k].apply(grads[k])
@@ -741,6 +748,8 @@ def test_pipeline_matches_serial_steps(gpu_device, no_device_errors, num_plans):
     np.testing.assert_array_equal(a.state.state0.cpu().numpy(), b.state.state0.cpu().numpy())
     with pytest.raises(ValueError):
         pipe.step(0, grads[0])
+    with pytest.raises(ValueError):
+        pipe.update(steps, grads[0])  # no forward of that step
     with pytest.raises(ValueError):
         PooledStepPipeline(pa[:1])
     no_device_errors()
