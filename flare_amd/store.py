@@ -591,6 +591,7 @@ class DynamicEmbeddingStore(EmbeddingStore):
         with torch.cuda.stream(self.stream):
             self.maps = {d: _KeyMap(_map_slots(self.capacity), self.device, self.stream) for d in self.tables}
         self._map_workspace = _Workspace(self.device)
+        self._row_bases: dict[int, tuple[int, torch.Tensor]] = {}  # dim -> (rows, [0, rows] on the device)
         torch.cuda.current_stream(self.device).wait_stream(self.stream)
 
     # -- keys -> rows -----------------------------------------------------------
@@ -736,12 +737,11 @@ class DynamicEmbeddingStore(EmbeddingStore):
 
     def _one_table(self, table: _TableState) -> torch.Tensor:
         """row_base of the whole table as one CSR table: [0, rows] (kept until the table grows)."""
-        cache = self.__dict__.setdefault("_row_bases", {})
-        hit = cache.get(table.dim)
+        hit = self._row_bases.get(table.dim)
         if hit is None or hit[0] != table.rows:
             base = torch.tensor([0, table.rows], dtype=torch.int64).pin_memory()
             hit = (table.rows, base.to(self.device, non_blocking=True))
-            cache[table.dim] = hit
+            self._row_bases[table.dim] = hit
         return hit[1]
 
     def lookup_pooled(self, keys: Any, offsets: Any, batch_size: int, dim: int, *, pooling: str = "sum",
@@ -1079,6 +1079,9 @@ class PooledStepPlan:
     def step(self, pooled_grad: torch.Tensor, normalization_steps: int = 1,
              grad_out: torch.Tensor | None = None, optimizer: Any = None) -> torch.Tensor:
         """Forward, dedup and apply of one training step, dedup overlapped with forward.
+
+        (Over a stream of batches, ``PooledStepPipeline`` is faster: it overlaps each batch's
+        dedup with the previous batch's update instead, where the two share the GPU better.)
 
         The dedup depends only on the ids, so it runs on a second stream (same
         default priority) while the forward pools rows on the shard's stream;
