@@ -1104,6 +1104,9 @@ int check_state(int mode, float *s0, float *s1, int32_t *step) {
 int check_workspace(const Workspace &need, size_t have) {
   if (have < need.total_bytes)
     return fail(FLARE_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", have, need.total_bytes);
+  // the layout starts at the workspace's first byte (the histograms) and its parts are
+  // read and written with 16-byte vectors
+  if (!aligned(need.hist, 16)) return fail(FLARE_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return FLARE_OK;
 }
 

@@ -150,3 +150,18 @@ def test_stream_and_zero_fill_validation_on_host():
     assert _call("flare_stream_create", None) == _native.ERR_ARGUMENT
     assert _call("flare_stream_destroy", None) == _native.ERR_ARGUMENT
     assert "null (default) stream" in _native.last_error()
+
+
+def test_misaligned_workspace_is_refused_on_host():
+    """The backward workspace is laid out from its first byte and used with 16-byte vectors:
+    a misaligned one is refused before any launch (ValueError, FLARE_ERR_WORKSPACE)."""
+    lib = _native.library()
+    n, rows, dim = 1000, 5000, 64
+    nbytes = lib.flare_pooled_backward_workspace_bytes(n, rows, dim)
+    fake = 1 << 40  # never dereferenced: validation fails first
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _native.call("flare_pooled_dedup", fake, _native.INT64, n, fake, 1, n, fake, rows, dim, 0,
+                     _native.LAYOUT_TABLE_MAJOR, None, None, None, fake + 8, nbytes, None)
+    with pytest.raises(ValueError, match="smaller than"):
+        _native.call("flare_pooled_dedup", fake, _native.INT64, n, fake, 1, n, fake, rows, dim, 0,
+                     _native.LAYOUT_TABLE_MAJOR, None, None, None, fake, nbytes - 1, None)
