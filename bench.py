@@ -959,12 +959,12 @@ def main() -> int:
             # PooledStepPipeline: forward; then this batch's update (its dedup ran beside the
             # previous update) while the next batch's dedup runs on the pipeline's stream.  A step
             # lasts from its forward to the next step's forward; the last one ends when the final
-            # dedup is done.
-            marks = dict.fromkeys(("forward_done", "update_start", "dedup_start", "dedup_done", "update_done"))
-            _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
+            # dedup is done.  Only the step boundaries and the end of the forward are marked here
+            # (each mark is a marker packet on the stream); the update and dedup phases are timed
+            # in an instrumented pass after this one.
+            marks = {"forward_done": None}
             pipe.step(args.warmup + i, grad, grad_out=grad_out, optimizer=none_opt, marks=marks)
-            ev[1], ev[4], ev[2], ev[3], ev[5] = (marks["forward_done"], marks["update_start"], marks["dedup_start"],
-                                                 marks["dedup_done"], marks["update_done"])
+            ev[1] = marks["forward_done"]
             if i > 0:
                 events[i - 1][6] = ev[0]
             if i + 1 == args.steps:
@@ -1002,6 +1002,23 @@ def main() -> int:
         ev[5].record(stream)
     torch.cuda.synchronize()
     wall1 = time.perf_counter()
+    # pipelined: the same steps again with every phase marked (the timing of the update's
+    # kernels and of the dedup beside them; not part of the value)
+    phase_events, phase_markers, phase_order = events, markers, order
+    if pipelined:
+        phase_events = [[None] * 7 for _ in range(args.steps)]
+        phase_order = []
+        for i in range(args.steps):
+            k = (args.warmup + args.steps + i) % len(plans)
+            phase_order.append(k)
+            marks = dict.fromkeys(("forward_done", "update_start", "dedup_start", "dedup_done", "update_done"))
+            _native.check(lib.flare_set_update_events(ctypes.cast(handles[i], ctypes.c_void_p), 4))
+            pipe.step(args.warmup + args.steps + i, grad, grad_out=grad_out, optimizer=none_opt, marks=marks)
+            ev = phase_events[i]
+            ev[1], ev[2], ev[3], ev[4], ev[5] = (marks["forward_done"], marks["dedup_start"], marks["dedup_done"],
+                                                 marks["update_start"], marks["update_done"])
+        pipe.finish()
+        torch.cuda.synchronize()
     stream_ctx.__exit__(None, None, None)
     _native.check(lib.flare_set_update_events(None, 0))
     timed_errors = int(lib.flare_take_device_errors(int(stream.cuda_stream)))
@@ -1017,26 +1034,30 @@ def main() -> int:
     step_ms, fwd_ms, dedup_ms, apply_ms = [], [], [], []
     step_gbs, fwd_gbs, upd_gbs = [], [], []
     sums_ms, fold_ms, applyk_ms, sums_gbs, applyk_gbs = [], [], [], [], []
-    for i, ev in enumerate(events):
+    for i, ev in enumerate(events):  # the timed steps: step and forward
         b = batches[order[i]]
         f = fwd_start[i].elapsed_time(ev[1])
         t = ev[0].elapsed_time(ev[6] if pipelined else ev[5])
-        a = ev[4].elapsed_time(ev[5])
         step_ms.append(t)
         fwd_ms.append(f)
-        dedup_ms.append(ev[2].elapsed_time(ev[3]))
-        apply_ms.append(a)
         fb, bb, ub = step_bytes(b.num_ids, uniques[order[i]], b.batch, b.num_tables, b.dim, s,
                                 b.weights is not None, b.optimizer, g_bytes)
         step_gbs.append((fb + bb) / (t * 1e-3) / 1e9)
         fwd_gbs.append(fb / (f * 1e-3) / 1e9)
+    for i, ev in enumerate(phase_events):  # dedup and update (the timed steps, or the marked pass)
+        b = batches[phase_order[i]]
+        a = ev[4].elapsed_time(ev[5])
+        dedup_ms.append(ev[2].elapsed_time(ev[3]))
+        apply_ms.append(a)
+        fb, bb, ub = step_bytes(b.num_ids, uniques[phase_order[i]], b.batch, b.num_tables, b.dim, s,
+                                b.weights is not None, b.optimizer, g_bytes)
         upd_gbs.append(ub / (a * 1e-3) / 1e9)
-        mk = markers[i]
+        mk = phase_markers[i]
         sm, fm, am = ev[4].elapsed_time(mk[0]), mk[0].elapsed_time(mk[1]), mk[1].elapsed_time(ev[5])
         sums_ms.append(sm)
         fold_ms.append(fm)
         applyk_ms.append(am)
-        sb, ab = kernel_bytes[order[i]]
+        sb, ab = kernel_bytes[phase_order[i]]
         sums_gbs.append(sb / (sm * 1e-3) / 1e9)
         applyk_gbs.append(ab / (am * 1e-3) / 1e9)
     med = statistics.median(step_ms)
@@ -1104,6 +1125,9 @@ def main() -> int:
         "hbm_gbs": achieved_step,
         "hbm_frac": achieved_step / PEAK_HBM_GBS,
         "algorithmic_bytes_per_step": fb0 + bb0,
+        "phases_source": (f"step and forward: the timed steps; dedup and update phases: {args.steps} further steps "
+                          "with every phase marked (the timed steps mark only step boundaries and the forward)"
+                          if pipelined else "the timed steps"),
         "phases_ms": {
             "forward_pooled_gather": statistics.median(fwd_ms),
             "dedup_sort_unique": statistics.median(dedup_ms),
