@@ -133,3 +133,30 @@ def test_dynamic_pooled_update_skips_keys_without_rows(gpu_device, no_device_err
     np.testing.assert_array_equal(table, expected)
     assert store.size(dim) == 3
     no_device_errors(1)
+
+
+def test_dynamic_pooled_update_rejects_nonfinite_gradients(gpu_device, no_device_errors):
+    """validate_values on the pooled step over keys: an inf in the pooled gradient raises
+    FloatingPointError and updates nothing; the same step with finite values then updates."""
+    from flare_amd.store import DynamicEmbeddingStore, RowWiseAdagrad, Uniform
+
+    dim, batch, features = 16, 50, 2
+    rng = np.random.default_rng(5)
+    keys = rng.integers(-(2 ** 40), 2 ** 40, size=features * batch).astype(np.int64)
+    offsets = np.arange(keys.size + 1, dtype=np.int64)
+    store = DynamicEmbeddingStore(400, [dim], value_dtype="bfloat16", optimizer=RowWiseAdagrad(lr=0.1),
+                                  initializer=Uniform(-0.5, 0.5), seed=8)
+    store.lookup_pooled(keys, offsets, batch, dim)
+    store.synchronize()
+    table0 = _host(store.tables[dim].table.clone())
+    grad = torch.full((features, batch, dim), 1e-3, dtype=torch.bfloat16, device=gpu_device)
+    grad[1, 7, 3] = float("inf")
+    with pytest.raises(FloatingPointError):
+        store.apply_pooled_gradients(keys, offsets, batch, grad, dim, validate_values=True)
+    store.synchronize()
+    np.testing.assert_array_equal(_host(store.tables[dim].table), table0)
+    grad[1, 7, 3] = 1e-3
+    store.apply_pooled_gradients(keys, offsets, batch, grad, dim, validate_values=True)
+    store.synchronize()
+    assert not np.array_equal(_host(store.tables[dim].table), table0)
+    no_device_errors(8)

@@ -753,3 +753,48 @@ def test_pipeline_matches_serial_steps(gpu_device, no_device_errors, num_plans):
     with pytest.raises(ValueError):
         PooledStepPipeline(pa[:1])
     no_device_errors()
+
+
+def test_pipeline_reduced_gradients_match_serial(gpu_device, no_device_errors):
+    """The pipeline with FLARE_OPT_NONE (reduced gradients written to grad_out, the table
+    untouched) over ragged weighted bags: grad_out and the dedup outputs of every step equal
+    those of the same steps run one phase after another."""
+    from flare_amd import _native
+    from flare_amd.store import PooledStepPipeline, PooledTableShard, RowWiseAdagrad, Uniform
+    from flare_amd.workload import make_workload, pooled_grad_host
+
+    ws = [make_workload(3, batch=300, row_scale=0.0005, batch_index=k) for k in range(2)]
+    w0 = ws[0]
+    none_opt = _native.FlareOptimizer()
+    none_opt.kind = _native.OPT_NONE
+
+    def shard():
+        return PooledTableShard(w0.table_rows, w0.dim, value_dtype=w0.value_dtype, optimizer=RowWiseAdagrad(),
+                                initializer=Uniform(-0.01, 0.01), seed=4, layout="table_major")
+
+    a, b = shard(), shard()
+    table0 = _host(a.table.clone())
+    pa = [a.plan_step(w.ids, w.offsets, w.batch, pooling="weighted", per_sample_weights=w.weights) for w in ws]
+    pb = [b.plan_step(w.ids, w.offsets, w.batch, pooling="weighted", per_sample_weights=w.weights) for w in ws]
+    grads = [torch.from_numpy(np.ascontiguousarray(pooled_grad_host(w).transpose(1, 0, 2))).to(gpu_device)
+             for w in ws]
+    n_max = max(w.num_ids for w in ws)
+    out_a = torch.empty((n_max, w0.dim), dtype=torch.float32, device=gpu_device)
+    out_b = torch.empty_like(out_a)
+    pipe = PooledStepPipeline(pa)
+    for i in range(5):
+        k = i % 2
+        pipe.step(i, grads[k], grad_out=out_a, optimizer=none_opt)
+        pb[k].forward()
+        pb[k].dedup()
+        pb[k].apply(grads[k], grad_out=out_b, optimizer=none_opt)
+        a.synchronize()
+        b.synchronize()
+        u = int(pb[k].unique_count.item())
+        assert int(pa[k].unique_count.item()) == u
+        np.testing.assert_array_equal(out_a[:u].cpu().numpy(), out_b[:u].cpu().numpy())
+        np.testing.assert_array_equal(pa[k].first_indices[:u].cpu().numpy(), pb[k].first_indices[:u].cpu().numpy())
+    pipe.finish()
+    a.synchronize()
+    np.testing.assert_array_equal(_host(a.table), table0)
+    no_device_errors()
