@@ -83,9 +83,11 @@ __device__ __forceinline__ int64_t xcd_block(int64_t i, int64_t blocks) {
   return x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
 }
 
-// Bags per lane group: 4 when the block stages its rows in LDS (32 KiB for
-// 128 bf16 rows of 128), 8 when rows are stored directly.
-constexpr int kBagsPerGroupStaged = 4;
+// Bags per lane group: 2 when the block stages its rows in LDS (16 KiB for
+// 64 bf16 rows of 128; against 4, it cuts the forward over bags of 1-8 ids,
+// 26 tables x 65536 bags of 128 bf16, from 416 to 407 us, and 8 is 527 us),
+// 8 when rows are stored directly.
+constexpr int kBagsPerGroupStaged = 2;
 constexpr int kBagsPerGroupDirect = 8;
 // Long bags (kLong: at least kLongBagLength ids per bag on average):
 // kLongDepth rows in flight, and one bag per lane group when groups are wide
@@ -98,6 +100,9 @@ constexpr int kBagsPerGroupDirect = 8;
 constexpr int64_t kLongBagLength = 8;
 constexpr int kLongDepth = 8;
 constexpr int kLongBagsNarrow = 4;
+// Rows in flight per lane for other bags (8 is slower: 474 against 407 us on
+// the workload above, from the registers it takes).
+constexpr int kRunDepth = 4;
 
 template <bool kStage, bool kLong>
 constexpr int bags_per_group(int g) {
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void pooled_kernel(PooledArgs a) {
   using R = RawVec<Tag, VEC>;
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
-  constexpr int kDepth = kLong ? kLongDepth : 4;
+  constexpr int kDepth = kLong ? kLongDepth : kRunDepth;
   __shared__ int64_t s_begin[kBagsPerBlock];
   __shared__ int64_t s_len[kBagsPerBlock];
   __shared__ int64_t s_lo[kBagsPerBlock];
