@@ -158,6 +158,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) v
   constexpr int kGroups = kThreads / G;
   constexpr int kBagsPerBlock = kGroups * kBagsPerGroup;
   constexpr int kDepth = kLong ? kLongDepth : kRunDepth;
+  static_assert(kDepth <= 32, "one bit of `live` per row in flight");
   __shared__ int64_t s_begin[kBagsPerBlock];
   __shared__ int64_t s_len[kBagsPerBlock];
   __shared__ int64_t s_lo[kBagsPerBlock];
