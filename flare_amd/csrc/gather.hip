@@ -83,11 +83,11 @@ __device__ __forceinline__ int64_t xcd_block(int64_t i, int64_t blocks) {
   return x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
 }
 
-// Bags per lane group: 2 when the block stages its rows in LDS (16 KiB for
-// 64 bf16 rows of 128; against 4, it cuts the forward over bags of 1-8 ids,
-// 26 tables x 65536 bags of 128 bf16, from 416 to 407 us, and 8 is 527 us),
-// 8 when rows are stored directly.
-constexpr int kBagsPerGroupStaged = 2;
+// Bags per lane group: 1 when the block stages its rows in LDS (8 KiB for 32
+// bf16 rows of 128; on the forward over bags of 1-8 ids, 26 tables x 65536
+// bags of 128 bf16, 1 bag took 337 us, 2 bags 370 us, 4 bags 429 us), 8 when
+// rows are stored directly.
+constexpr int kBagsPerGroupStaged = 1;
 constexpr int kBagsPerGroupDirect = 8;
 // Long bags (kLong: at least kLongBagLength ids per bag on average):
 // kLongDepth rows in flight, and one bag per lane group when groups are wide
@@ -100,7 +100,7 @@ constexpr int kBagsPerGroupDirect = 8;
 constexpr int64_t kLongBagLength = 8;
 constexpr int kLongDepth = 8;
 constexpr int kLongBagsNarrow = 4;
-// Rows in flight per lane for other bags (8 is slower: 474 against 407 us on
+// Rows in flight per lane for other bags (8 was slower: 474 against 407 us on
 // the workload above, from the registers it takes).
 constexpr int kRunDepth = 4;
 
@@ -148,7 +148,8 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // is stored when finished.
 // Five waves per SIMD: the compiler keeps the kernel within 96 VGPRs (a few
 // bytes spill in some instantiations).  On bags of 1-8 ids (26 tables x 65536
-// bags of 128 bf16) that took the forward from 400 to 370 us; long bags
+// bags of 128 bf16, 2 bags per lane group) that took the forward from 400 to
+// 370 us; long bags
 // (geometric(30) fp16 rows of 64, U[1,64] bf16 rows of 128) were unchanged.
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void pooled_kernel(PooledArgs a) {
