@@ -70,3 +70,26 @@ def test_step_bytes_follow_the_published_formula():
     assert bwd_adam == n * 8 + offsets + b * t * d * 4 + u * 8 + n * 4 + 2 * u * d * s + 2 * u * (2 * d * 4 + 4)
     _, bwd_none, _ = bench.step_bytes(n, u, b, t, d, s, False, "none")
     assert bwd_none == n * 8 + offsets + b * t * d * 4 + u * 8 + n * 4 + u * d * 4
+
+
+def test_committed_traffic_covers_each_workloads_long_kernels():
+    # roofline.traffic reads the committed counter runs: every workload needs its forward and its
+    # two update kernels there, and each counter's copy calibration must be the one the counters
+    # give on this GPU (FETCH_SIZE counts half of a copy's read bytes, WRITE_SIZE all written ones)
+    expected = {1: ("pooled_kernel", "piece_sums_kernel", "key_apply_kernel"),
+                2: ("pooled_one_kernel", "piece_sums_kernel", "key_apply_kernel"),
+                3: ("pooled_kernel", "sums_kernel", "apply_kernel"),
+                4: ("pooled_kernel", "piece_sums_kernel", "key_apply_kernel"),
+                5: ("pooled_kernel", "piece_sums_kernel", "key_apply_kernel")}
+    import json
+
+    recs = json.loads((Path(bench.ROOT) / "profiles" / "step_kernel_traffic.json").read_text())["workloads"]
+    for config, kernels in expected.items():
+        rec = recs[str(config)]
+        assert 1.9 < rec["fetch_scale"] < 2.1 and 0.95 < rec["write_scale"] < 1.05, config
+        assert (Path(bench.ROOT) / rec["summary"]).exists(), config
+        for k in kernels:
+            traffic = bench.kernel_traffic(config, k)
+            assert traffic is not None and traffic > 0, (config, k)
+    assert bench.kernel_traffic(2, "no_such_kernel") is None
+    assert bench.kernel_traffic(9, "pooled_kernel") is None
