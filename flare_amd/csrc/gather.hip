@@ -138,7 +138,8 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // pools kBagsPerGroup of those bags: it streams their ids as one virtual run
 // (G ids per lane-parallel load, each lane finding its bag from the running
 // lengths), gathers rows kDepth at a time regardless of bag boundaries
-// (packed, so four rows of loads are in flight per lane), accumulates in
+// (packed: kRunDepth, or kLongDepth for long bags, rows of loads in flight
+// per lane), accumulates in
 // occurrence order, and emits a bag's pooled row when the stream passes the
 // bag's end.  Lane l holds L vectors of VEC elements at columns (q*G + l)*VEC.
 // kStage: finished rows go to LDS and the block writes its whole range once,
@@ -149,8 +150,8 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // Five waves per SIMD: the compiler keeps the kernel within 96 VGPRs (a few
 // bytes spill in some instantiations).  On bags of 1-8 ids (26 tables x 65536
 // bags of 128 bf16, 2 bags per lane group) that took the forward from 400 to
-// 370 us; long bags
-// (geometric(30) fp16 rows of 64, U[1,64] bf16 rows of 128) were unchanged.
+// 370 us; long bags (geometric(30) fp16 rows of 64, U[1,64] bf16 rows of 128)
+// were unchanged.
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void pooled_kernel(PooledArgs a) {
   constexpr int kBagsPerGroup = bags_per_group<kStage, kLong>(G);
