@@ -147,13 +147,19 @@ __device__ __forceinline__ int64_t resolve_row(const PooledArgs &a, int64_t i, i
 // wave's loads and stores share one in-order completion counter, so stores
 // issued between loads would lengthen every later wait).  Otherwise each row
 // is stored when finished.
-// Five waves per SIMD: the compiler keeps the kernel within 96 VGPRs (a few
-// bytes spill in some instantiations).  On bags of 1-8 ids (26 tables x 65536
-// bags of 128 bf16, 2 bags per lane group) that took the forward from 400 to
-// 370 us; long bags (geometric(30) fp16 rows of 64, U[1,64] bf16 rows of 128)
-// were unchanged.
+// Minimum waves per SIMD asked of the compiler.  Five (at most 96 VGPRs) for
+// staged blocks: on bags of 1-8 ids (26 tables x 65536 bags of 128 bf16, then
+// 2 bags per lane group) that took the forward from 400 to 370 us.  Long bags
+// in narrow groups keep their own allocation: four bags per group leave few
+// enough waves to be resident at once (8 x 16384 bags of 64 fp16), and five
+// would spill.  Unstaged blocks (8 bags per group) would spill too.
+template <bool kStage, bool kLong>
+constexpr int pooled_min_waves(int g) {
+  return (kStage && !(kLong && g <= 8)) ? 5 : 1;
+}
+
 template <typename Tag, int VEC, int G, int L, bool kCsr, typename IdT, bool kStage, bool kLong>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void pooled_kernel(PooledArgs a) {
+__global__ __launch_bounds__(kThreads, (pooled_min_waves<kStage, kLong>(G))) void pooled_kernel(PooledArgs a) {
   constexpr int kBagsPerGroup = bags_per_group<kStage, kLong>(G);
   using E = typename Tag::elem;
   using R = RawVec<Tag, VEC>;
